@@ -1,0 +1,287 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention path at the BASELINE.json configs.
+
+One JSON line on stdout.  The headline (`value`) is config C2: decode of one
+token over a 32768-row f16 KV cache (16 query / 2 KV heads, head_dim 256,
+sigmoid gate), reported as whole-call HBM GB/s.  One "step" runs that decode
+over the 10 full-attention layers of Qwen3.6 (a distinct 64 MiB cache per
+layer, so each launch reads K/V from HBM, not from the 256 MB last-level
+cache).  Also reported: C4 causal prefill (4096 tokens, TFLOP/s), C5 K=4
+verify at 65536 + rollback, C3 ragged 64-sequence decode, each with its
+dominant kernel's duration from HIP events on its launch stream, and the CPU
+baseline (the oracle's restatement of the reference CPU attention, one
+thread) on a bounded sample of the C2 shape.
+
+Timing: launches are queued behind a GPU sleep so that the timed region
+measures device execution, not Python enqueue cost; a barrier-free
+single-process run (--gpus 1 only).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+H, G, D = 16, 2, 256
+LAYERS = 10            # full-attention layers of Qwen3.6-35B-A3B
+C2_CTX = 32768
+C2_BYTES = 67_133_440  # K+V 67,108,864 + q, gate, out 3 x 8,192
+C4_N = 4096
+C4_FLOP = 4 * H * D * C4_N * (C4_N + 1) // 2  # QK^T + PV over causal pairs
+C5_CTX, C5_K = 65536, 4
+C5_BYTES = 134_324_224
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="bounded CPU-baseline sample length")
+    p.add_argument("--only", default="", help="comma list of decode,prefill,verify,ragged")
+    return p.parse_args()
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is "
+                          "designed but not built (DESIGN.md)", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import moe_infer_amd as mi
+    from moe_infer_amd import _lib
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    only = set(filter(None, args.only.split(",")))
+    hbm_peak, f16_peak = _lib.peaks()
+
+    def randn(*shape, seed):
+        gen.manual_seed(seed)
+        return torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32).half()
+
+    # GPU sleep calibration: cycles per millisecond of torch.cuda._sleep
+    def calib_sleep():
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1000)
+        torch.cuda.synchronize()
+        s.record()
+        torch.cuda._sleep(1_000_000)
+        e.record()
+        torch.cuda.synchronize()
+        return 1_000_000 / max(s.elapsed_time(e), 1e-3)
+
+    cyc_per_ms = calib_sleep()
+
+    def timed(fn, steps, warmup, backlog_ms):
+        """Runs fn() warmup + steps times; the timed steps are queued behind
+        a GPU sleep of backlog_ms so events bracket device time only."""
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        _lib.prof_enable(True)
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(int(backlog_ms * cyc_per_ms))
+        s.record()
+        for _ in range(steps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / steps  # ms per step
+
+    print(f"[bench] start; sleep calib {cyc_per_ms:.0f} cycles/ms", file=sys.stderr, flush=True)
+    rec = {}
+
+    # ---------------------------------------------------------------- C2 decode
+    if not only or "decode" in only:
+        cache = mi.Cache(num_layers=LAYERS, capacity=C2_CTX)
+        for layer in range(LAYERS):
+            k = randn(C2_CTX, G * D, seed=200 + layer)
+            v = randn(C2_CTX, G * D, seed=300 + layer)
+            mi.kv_cache_append(cache, layer, k, v, 0)
+            del k, v
+        cache.set_pos(C2_CTX)
+        qs = [randn(H * D, seed=400 + i) for i in range(LAYERS)]
+        gs = [randn(H * D, seed=500 + i) for i in range(LAYERS)]
+        outs = [torch.empty(H * D, dtype=torch.float16, device=dev) for _ in range(LAYERS)]
+
+        def decode_step():
+            for layer in range(LAYERS):
+                mi.attn_decode(cache, layer, qs[layer], C2_CTX, gate=gs[layer], out=outs[layer])
+
+        ms = timed(decode_step, args.steps, args.warmup,
+                   backlog_ms=args.steps * LAYERS * 0.25 + 20)
+        split_us, n_split = _lib.prof_read("attn_split")
+        comb_us, _ = _lib.prof_read("attn_combine")
+        _lib.prof_enable(False)
+        us_layer = ms * 1000 / LAYERS
+        rec["decode"] = {
+            "us_per_layer": us_layer, "gbps": C2_BYTES / (us_layer * 1e3),
+            "split_kernel_us": split_us, "combine_kernel_us": comb_us, "launches": n_split,
+            "bytes_per_layer": C2_BYTES, "ms_per_step": ms,
+        }
+        print(f"[bench] decode {us_layer:.2f} us/layer split {split_us:.2f} us", file=sys.stderr,
+              flush=True)
+        del cache
+
+    # --------------------------------------------------------------- C4 prefill
+    if not only or "prefill" in only:
+        cache = mi.Cache(num_layers=1, capacity=C4_N)
+        q = randn(C4_N, H, D, seed=41)
+        k = randn(C4_N, G * D, seed=42)
+        v = randn(C4_N, G * D, seed=43)
+        out = torch.empty_like(q)
+
+        def prefill_step():
+            mi.attn_prefill(cache, 0, q, k, v, 0, out=out)
+
+        psteps = max(args.steps, 10)
+        ms = timed(prefill_step, psteps, args.warmup, backlog_ms=30)
+        pk_us, _ = _lib.prof_read("attn_prefill")
+        ap_us, _ = _lib.prof_read("kv_append")
+        _lib.prof_enable(False)
+        rec["prefill"] = {
+            "ms_per_step": ms, "kernel_us": pk_us, "append_us": ap_us,
+            "tflops_kernel": C4_FLOP / (pk_us * 1e6), "tflops_step": C4_FLOP / (ms * 1e9),
+            "flop": C4_FLOP,
+        }
+        print(f"[bench] prefill {ms * 1000:.1f} us/step kernel {pk_us:.1f} us "
+              f"= {C4_FLOP / (pk_us * 1e6):.1f} TFLOP/s", file=sys.stderr, flush=True)
+        del cache
+
+    # ---------------------------------------------------------------- C5 verify
+    if not only or "verify" in only:
+        nl = 4  # 4 x 128 MiB of K/V: more than the last-level cache
+        cache = mi.Cache(num_layers=nl, capacity=C5_CTX + C5_K)
+        for layer in range(nl):
+            mi.kv_cache_append(cache, layer, randn(C5_CTX, G * D, seed=600 + layer),
+                               randn(C5_CTX, G * D, seed=700 + layer), 0)
+        q = randn(C5_K, H, D, seed=51)
+        k = randn(C5_K, G * D, seed=52)
+        v = randn(C5_K, G * D, seed=53)
+        g = randn(C5_K, H, D, seed=54)
+        out = torch.empty_like(q)
+
+        def verify_step():
+            for layer in range(nl):
+                mi.attn_verify(cache, layer, q, k, v, C5_CTX, gate=g, out=out)
+            cache.set_pos(C5_CTX + 2)  # accept 2 drafts, roll back the rest
+
+        ms = timed(verify_step, args.steps, args.warmup, backlog_ms=args.steps * nl * 0.3 + 20)
+        split_us, _ = _lib.prof_read("attn_split")
+        _lib.prof_enable(False)
+        us_call = ms * 1000 / nl
+        rec["verify"] = {"us_per_layer": us_call, "gbps": C5_BYTES / (us_call * 1e3),
+                         "split_kernel_us": split_us, "bytes": C5_BYTES}
+        print(f"[bench] verify {us_call:.2f} us/layer", file=sys.stderr, flush=True)
+        del cache
+
+    # ---------------------------------------------------------------- C3 ragged
+    if not only or "ragged" in only:
+        rng = np.random.default_rng(3)
+        lengths = rng.integers(1024, 32769, size=64).astype(np.int32)
+        offsets = np.zeros(64, np.int32)
+        offsets[1:] = np.cumsum((lengths + 7) // 8 * 8)[:-1]
+        rows = int(offsets[-1] + (lengths[-1] + 7) // 8 * 8)
+        k = randn(rows, G * D, seed=31)
+        vb = mi.kv_pack_v(randn(rows, G * D, seed=32), G)
+        q = randn(64, H, D, seed=33)
+        g = randn(64, H, D, seed=34)
+        out = torch.empty_like(q)
+        off_t = torch.from_numpy(offsets).to(dev)
+        len_t = torch.from_numpy(lengths).to(dev)
+        ws = mi.ragged_workspace(64, 32768, device=dev)
+        mi.attn_decode_ragged(k, vb, off_t, len_t, q, 32768, gate=g, out=out, workspace=ws)
+
+        def ragged_step():
+            mi.attn_decode_ragged(k, vb, off_t, len_t, q, 32768, gate=g, out=out, workspace=ws,
+                                  validate=False)
+
+        ms = timed(ragged_step, args.steps, args.warmup, backlog_ms=20)
+        split_us, _ = _lib.prof_read("attn_split")
+        _lib.prof_enable(False)
+        rbytes = 2048 * int(lengths.sum()) + 64 * 24576
+        rec["ragged"] = {"us_per_step": ms * 1000, "gbps": rbytes / (ms * 1e6),
+                         "split_kernel_us": split_us, "bytes": rbytes,
+                         "sum_len": int(lengths.sum())}
+        print(f"[bench] ragged {ms * 1000:.1f} us", file=sys.stderr, flush=True)
+        del k, vb
+
+    # -------------------------------------------------------------- CPU baseline
+    cpu = None
+    if (not only or "decode" in only) and args.cpu_seconds > 0:
+        from oracle import oracle as O
+        rng = np.random.default_rng(2)
+        qh = rng.standard_normal(H * D, dtype=np.float32).astype(np.float16)
+        kh = rng.standard_normal((C2_CTX, G * D), dtype=np.float32).astype(np.float16)
+        vh = rng.standard_normal((C2_CTX, G * D), dtype=np.float32).astype(np.float16)
+        gh = rng.standard_normal(H * D, dtype=np.float32).astype(np.float16)
+        O.decode(qh, kh, vh, 16, gate=gh)  # load the library
+        t0, runs = time.perf_counter(), 0
+        while True:
+            O.decode(qh, kh, vh, C2_CTX, gate=gh)
+            runs += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds:
+                break
+        us = el / runs * 1e6
+        cpu = {"value": C2_BYTES / (us * 1e3), "unit": "GB/s", "cores": 1, "kind": "port",
+               "us_per_layer": us,
+               "sample": f"{runs} single-thread C2 decodes (ctx 32768, gated) of the C "
+                         f"restatement of src/math_util.rs:323-392 in {el:.1f} s; host "
+                         f"nproc={os.cpu_count()}"}
+
+    d = rec.get("decode")
+    p = rec.get("prefill")
+    line = {
+        "metric": "decode attn µs/layer + HBM GB/s @ctx 32K; prefill TFLOP/s @4K tokens",
+        "value": round(d["gbps"], 2) if d else None,
+        "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(d["ms_per_step"], 4) if d else None,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic (seeded N(0,1) f16 q/K/V/gate)",
+        "config": {"workload": "C2: GQA decode, 1 token, ctx 32768, 16q/2kv heads, head_dim "
+                               "256, f16 KV, sigmoid gate; step = 10 full-attention layers",
+                   "batch": 1, "ctx": C2_CTX, "layers_per_step": LAYERS},
+    }
+    if d:
+        line["decode_us_per_layer"] = round(d["us_per_layer"], 3)
+        ach = C2_BYTES / (d["split_kernel_us"] * 1e3)
+        line["roofline"] = {"bound": "hbm", "kernel": "attn_split_kernel (decode, C2)",
+                            "achieved": round(ach, 1), "peak": hbm_peak, "unit": "GB/s",
+                            "frac": round(ach / hbm_peak, 4), "traffic": None}
+        line["decode"] = {k2: (round(v2, 3) if isinstance(v2, float) else v2)
+                          for k2, v2 in d.items()}
+    if p:
+        line["prefill_tflops"] = round(p["tflops_kernel"], 1)
+        line["roofline_prefill"] = {"bound": "mfma", "kernel": "attn_prefill_kernel (C4)",
+                                    "achieved": round(p["tflops_kernel"], 1), "peak": f16_peak,
+                                    "unit": "TFLOP/s",
+                                    "frac": round(p["tflops_kernel"] / f16_peak, 4),
+                                    "traffic": None}
+        line["prefill"] = {k2: (round(v2, 3) if isinstance(v2, float) else v2)
+                           for k2, v2 in p.items()}
+    for key in ("verify", "ragged"):
+        if key in rec:
+            line[key] = {k2: (round(v2, 3) if isinstance(v2, float) else v2)
+                         for k2, v2 in rec[key].items()}
+    line["cpu_baseline"] = cpu
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

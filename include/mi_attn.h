@@ -1,0 +1,217 @@
+/*
+ * mi_attn.h — C ABI of the MI355X (gfx950) attention library for the
+ * Qwen3.6 full-attention layers: GQA decode over an f16 KV cache, causal
+ * batched prefill, K-token speculative verify, ragged batched decode, and the
+ * KV-cache append / reset / rollback state those steps read and write.
+ *
+ * Conventions
+ *   - Every entry point returns an mi_status; nothing aborts across the ABI.
+ *     On failure mi_last_error() returns a thread-local description.
+ *   - Tensor arguments are DEVICE pointers unless the parameter name starts
+ *     with "host_".  f16 values are IEEE binary16 bit patterns (mi_f16).
+ *   - Work is enqueued on the caller's stream (a hipStream_t passed as void*;
+ *     NULL is the legacy default stream) and is asynchronous unless the name
+ *     ends in _sync.  A handle is not internally synchronised: use one handle
+ *     per thread (the reference's pyclasses are `unsendable`).
+ *   - Shapes: H query heads, G KV heads, head dim D.  The kernels are built
+ *     for the Qwen3.6 full-attention shape D = 256, H / G = 8; other shapes
+ *     return MI_ERR_UNSUPPORTED.  Softmax scale is 1/sqrt(D), accumulation f32.
+ *
+ * Logical KV layout is the reference's token-major K[pos][kvh*D + i]
+ * (src/math_util.rs:336).  Physical layout on the device (what
+ * mi_kv_layer_ptrs and mi_attn_decode_ragged see):
+ *   K: token-major, row r at  K + r*G*D            (unchanged from the reference)
+ *   V: 8-row transposed blocks: element (r, h, i) at
+ *        V + ((r/8)*G + h)*D*8 + i*8 + (r%8)
+ *      so the eight keys of one value column are one 16-byte load.
+ * mi_kv_upload / mi_kv_download convert to and from token-major host rows, so
+ * callers that move cache contents through the host see the reference layout.
+ */
+#ifndef MI_ATTN_H
+#define MI_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t mi_f16;
+typedef void* mi_stream;
+
+typedef enum mi_status {
+  MI_OK = 0,
+  MI_ERR_INVALID_ARG = 1,   /* null pointer, bad layer, n <= 0, bad shape   */
+  MI_ERR_OUT_OF_RANGE = 2,  /* position beyond capacity / sequence length   */
+  MI_ERR_OOM = 3,           /* device allocation failed                     */
+  MI_ERR_HIP = 4,           /* a HIP runtime call failed                    */
+  MI_ERR_UNSUPPORTED = 5    /* head shape the kernels are not built for     */
+} mi_status;
+
+/* Rows per V block of the device layout, and the granularity capacities are
+ * rounded up to. */
+#define MI_KV_VBLOCK 8
+#define MI_KV_CAP_ALIGN 256
+
+/* Roofline constants every measurement in this project divides by
+ * (MI355X datasheet: HBM3E 8.0 TB/s, dense f16 MFMA 2.5 PFLOP/s). */
+#define MI_PEAK_HBM_GBPS 8000.0
+#define MI_PEAK_F16_TFLOPS 2500.0
+
+/* ---------------------------------------------------------------- errors -- */
+
+/* Thread-local message of the last failed call on this thread ("" if none).
+ * Replaces MoEError's Display (src/error.rs:4-9). */
+const char* mi_last_error(void);
+
+/* Version / build string, e.g. "mi_attn 0.1 gfx950". */
+const char* mi_version(void);
+
+/* Writes MI_PEAK_HBM_GBPS and MI_PEAK_F16_TFLOPS (for bindings that cannot
+ * read macros). */
+void mi_roofline_peaks(double* hbm_gbps, double* f16_tflops);
+
+/* -------------------------------------------------------------- KV cache -- */
+
+typedef struct mi_kv mi_kv;
+
+/* Per-full-attention-layer K/V store plus `pos` and per-layer `len`.
+ * Replaces Cache::new (src/cache.rs:45-76) and the GPU buffers of
+ * MetalContext (src/engine/qwen35_moe/metal_context.rs:316-319, 492-502).
+ * `num_layers` counts full-attention layers only (the reference's Linear
+ * layers hold no KV).  Capacity is rounded up to MI_KV_CAP_ALIGN rows; new
+ * memory is zero-filled.  Blocks until allocation and clearing finish. */
+mi_status mi_kv_create(int32_t num_layers, int32_t num_q_heads,
+                       int32_t num_kv_heads, int32_t head_dim,
+                       int64_t capacity, mi_kv** out);
+void mi_kv_destroy(mi_kv* kv);
+
+/* Grow to at least `capacity` rows, keeping every existing row (including
+ * stale rows past len, as metal_context.rs:368-431 copies the whole old
+ * buffer).  Never shrinks.  Synchronous. */
+mi_status mi_kv_reserve(mi_kv* kv, int64_t capacity);
+mi_status mi_kv_capacity(const mi_kv* kv, int64_t* capacity);
+mi_status mi_kv_shape(const mi_kv* kv, int32_t* num_layers, int32_t* num_q_heads,
+                      int32_t* num_kv_heads, int32_t* head_dim);
+
+/* Cache::set_pos (src/cache.rs:102-109): pos = p and len = p on every layer.
+ * Rollback is position-only: no row is modified. */
+mi_status mi_kv_set_pos(mi_kv* kv, int64_t pos);
+/* Cache::reset (src/cache.rs:84-94) restricted to KV state: set_pos(0). */
+mi_status mi_kv_reset(mi_kv* kv);
+mi_status mi_kv_pos(const mi_kv* kv, int64_t* pos);
+mi_status mi_kv_len(const mi_kv* kv, int32_t layer, int64_t* len);
+/* FullState::len of one layer (src/cache.rs:273-287); p <= capacity. */
+mi_status mi_kv_set_len(mi_kv* kv, int32_t layer, int64_t len);
+
+/* Device base pointers of one layer (physical layout above). */
+mi_status mi_kv_layer_ptrs(mi_kv* kv, int32_t layer, mi_f16** k, mi_f16** v);
+
+/* kv_cache_append / kv_cache_append_n (src/math_util.rs:387-392,
+ * src/engine/shaders.metal:2370-2383, 2774-2792): bit copy of n rows of
+ * G*D values from k[n][G*D], v[n][G*D] into rows [pos, pos+n); then
+ * len(layer) = pos + n (src/engine/qwen35_moe/cpu.rs:144).  Grows the cache
+ * (synchronously) when pos + n exceeds capacity. */
+mi_status mi_kv_append(mi_kv* kv, int32_t layer, const mi_f16* k,
+                       const mi_f16* v, int64_t pos, int32_t n,
+                       mi_stream stream);
+
+/* Host <-> device copies of rows [row0, row0+rows) of one layer in
+ * token-major order (MetalContext::upload_cache / download_cache,
+ * metal_context.rs:804-882).  Synchronous.  Upload does not change len. */
+mi_status mi_kv_upload(mi_kv* kv, int32_t layer, const mi_f16* host_k,
+                       const mi_f16* host_v, int64_t row0, int64_t rows);
+mi_status mi_kv_download(const mi_kv* kv, int32_t layer, mi_f16* host_k,
+                         mi_f16* host_v, int64_t row0, int64_t rows);
+
+/* Cache::copy_from (src/cache.rs:112-128): copies every row of every layer,
+ * pos and len.  Shapes must match; dst grows to src's capacity.  Synchronous. */
+mi_status mi_kv_copy_from(mi_kv* dst, const mi_kv* src);
+
+/* ------------------------------------------------------------- attention -- */
+
+/* Decode attention of one query token over rows [0, seq_len) of `layer`:
+ * out[h] = softmax(q_h . K^T / sqrt(D)) V  for every query head h, KV head
+ * h / (H/G); then out *= sigmoid(gate) elementwise when gate != NULL.
+ * q, gate, out: [H*D] f16.  Split-K flash-decoding plus a combine kernel.
+ * Semantics: attention_scores/softmax/values_batched + sigmoid_gate_inplace
+ * (src/math_util.rs:264-269, 323-383), kernels attn_sdpa_block +
+ * attn_sdpa_reduce (src/engine/shaders.metal:1559-1776).  seq_len == 0 gives
+ * zeros (the reference's zero-filled output, math_util.rs:372). */
+mi_status mi_attn_decode(mi_kv* kv, int32_t layer, const mi_f16* q,
+                         const mi_f16* gate, mi_f16* out, int64_t seq_len,
+                         mi_stream stream);
+
+/* The engine's full-attention step for one token (encode_pre_expert_full,
+ * src/engine/qwen35_moe/fused_exp2.rs:669-733; cpu.rs:136-167): append k, v
+ * ([G*D] f16) at `pos`, then decode with seq_len = pos + 1 and gate.
+ * Leaves pos(kv) unchanged: the engine advances it once per token, after
+ * its last layer, with mi_kv_set_pos(pos + 1) (fused_exp2.rs:1030-1031). */
+mi_status mi_attn_step(mi_kv* kv, int32_t layer, const mi_f16* q,
+                       const mi_f16* k, const mi_f16* v, const mi_f16* gate,
+                       mi_f16* out, int64_t pos, mi_stream stream);
+
+/* Causal batched prefill (op1_full_batched, src/engine/qwen35_moe/
+ * batched.rs:233-260; kernels kv_cache_append_n + attn_sdpa_causal_n,
+ * shaders.metal:2656-2792): append n rows k, v [n][G*D] at past_pos, then
+ * query i (q [n][H][D]) attends rows [0, past_pos + i] inclusive; gate
+ * [n][H][D] or NULL; out [n][H][D].  MFMA flash-attention kernel. */
+mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
+                          const mi_f16* k, const mi_f16* v, const mi_f16* gate,
+                          mi_f16* out, int64_t past_pos, int32_t n,
+                          mi_stream stream);
+
+/* K-token verify for speculative decoding: same contract as mi_attn_prefill
+ * (append at past_pos, query i attends [0, past_pos + i]) for small n, run
+ * as a split-K HBM-bound kernel over the cache instead of the MFMA prefill
+ * tiles.  Rollback afterwards is mi_kv_set_pos. */
+mi_status mi_attn_verify(mi_kv* kv, int32_t layer, const mi_f16* q,
+                         const mi_f16* k, const mi_f16* v, const mi_f16* gate,
+                         mi_f16* out, int64_t past_pos, int32_t n,
+                         mi_stream stream);
+
+/* Ragged batched decode: `batch` independent sequences, one query token
+ * each.  Sequence s owns rows [offsets[s], offsets[s] + lengths[s]) of the
+ * shared k_rows / v_rows buffers (physical layout above with G KV heads;
+ * offsets must be multiples of MI_KV_VBLOCK, the V buffer must hold whole
+ * blocks).  offsets, lengths: device int32[batch].  q, gate, out:
+ * [batch][H][D].  max_len >= every lengths[s] bounds the launch grid.
+ * No reference counterpart (the reference decodes one sequence,
+ * README.md:150-165); per-sequence math is mi_attn_decode's.  Needs a
+ * device workspace of mi_attn_ragged_workspace_size bytes. */
+size_t mi_attn_ragged_workspace_size(int32_t batch, int32_t max_len,
+                                     int32_t num_q_heads, int32_t num_kv_heads,
+                                     int32_t head_dim);
+mi_status mi_attn_decode_ragged(const mi_f16* k_rows, const mi_f16* v_rows,
+                                const int32_t* offsets, const int32_t* lengths,
+                                int32_t batch, int32_t max_len,
+                                int32_t num_q_heads, int32_t num_kv_heads,
+                                int32_t head_dim, const mi_f16* q,
+                                const mi_f16* gate, mi_f16* out,
+                                void* workspace, size_t workspace_bytes,
+                                mi_stream stream);
+
+/* Layout helpers for callers that build ragged buffers themselves: convert
+ * `rows` token-major rows ([rows][G*D]) into the device V block layout
+ * starting at block-aligned row `row0` of dst (device pointers, async). */
+mi_status mi_kv_pack_v(const mi_f16* src_rows, mi_f16* dst_v, int64_t row0,
+                       int64_t rows, int32_t num_kv_heads, int32_t head_dim,
+                       mi_stream stream);
+
+/* ------------------------------------------------------------- profiling -- */
+
+/* Kernel timing with HIP events on each launch's stream (the reference's
+ * telemetry counterpart, src/engine.rs:13-24, at kernel granularity).
+ * mi_prof_enable synchronises the device and clears earlier records.
+ * Kernel names: "attn_split", "attn_combine", "attn_prefill", "kv_append".
+ * mi_prof_read returns the mean duration in microseconds and the number of
+ * launches recorded since the last enable. */
+void mi_prof_enable(int on);
+mi_status mi_prof_read(const char* kernel, double* avg_us, int64_t* count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI_ATTN_H */

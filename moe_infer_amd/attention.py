@@ -1,0 +1,180 @@
+"""Tensor-level entry points of the gfx950 attention library.
+
+Each function validates shapes, dtypes and devices on the host, then calls
+the C ABI (include/mi_attn.h) on the current HIP stream.  Tensors are torch
+f16 CUDA tensors, contiguous.  H query heads, G KV heads, D = 256.
+
+Reference operators these stand for (fbundle/moe_infer):
+  attn_decode   attention_scores/softmax/values_batched + sigmoid_gate_inplace
+                (src/math_util.rs:264-269, 323-383); Metal attn_sdpa_block +
+                attn_sdpa_reduce (src/engine/shaders.metal:1559-1776)
+  attn_step     the engine's append-then-attend step
+                (src/engine/qwen35_moe/cpu.rs:136-167, fused_exp2.rs:669-733)
+  attn_prefill  kv_cache_append_n + attn_sdpa_causal_n + sigmoid_gate
+                (src/engine/qwen35_moe/batched.rs:233-260)
+  attn_verify   attn_sdpa_causal_n with past_pos = ctx and n = K drafts
+  attn_decode_ragged  (no reference counterpart) independent sequences
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import _lib
+
+HEAD_DIM = 256
+KV_VBLOCK = 8
+
+
+def _stream() -> C.c_void_p:
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> C.c_void_p | None:
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _check_tensor(name: str, t: torch.Tensor, numel: int, dtype=torch.float16) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a GPU tensor, got {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.numel() != numel:
+        raise ValueError(f"{name} has {t.numel()} elements, expected {numel}")
+    if t.data_ptr() % 16:
+        raise ValueError(f"{name} must be 16-byte aligned")
+
+
+def _check_qgo(cache, q, gate, out, n):
+    H, D = cache.num_q_heads, cache.head_dim
+    _check_tensor("q", q, n * H * D)
+    if gate is not None:
+        _check_tensor("gate", gate, n * H * D)
+    if out is None:
+        out = torch.empty_like(q)
+    _check_tensor("out", out, n * H * D)
+    return out
+
+
+def _check_kv_rows(cache, k, v, n):
+    G, D = cache.num_kv_heads, cache.head_dim
+    _check_tensor("k", k, n * G * D)
+    _check_tensor("v", v, n * G * D)
+
+
+def kv_cache_append(cache, layer: int, k: torch.Tensor, v: torch.Tensor, pos: int) -> None:
+    """Writes n rows k, v ([n, G*D]) at rows [pos, pos+n) of `layer`;
+    len(layer) = pos + n."""
+    n = k.numel() // (cache.num_kv_heads * cache.head_dim)
+    _check_kv_rows(cache, k, v, n)
+    _lib.check(_lib.lib().mi_kv_append(cache._h, cache.slot(layer), _ptr(k), _ptr(v),
+                                       int(pos), n, _stream()))
+
+
+def attn_decode(cache, layer: int, q: torch.Tensor, seq_len: int,
+                gate: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """One query token ([H, D] or [H*D]) over rows [0, seq_len) of `layer`."""
+    out = _check_qgo(cache, q, gate, out, 1)
+    _lib.check(_lib.lib().mi_attn_decode(cache._h, cache.slot(layer), _ptr(q), _ptr(gate),
+                                         _ptr(out), int(seq_len), _stream()))
+    return out
+
+
+def attn_step(cache, layer: int, q, k, v, pos: int, gate=None, out=None) -> torch.Tensor:
+    """Append k, v at `pos`, then decode with seq_len = pos + 1."""
+    out = _check_qgo(cache, q, gate, out, 1)
+    _check_kv_rows(cache, k, v, 1)
+    _lib.check(_lib.lib().mi_attn_step(cache._h, cache.slot(layer), _ptr(q), _ptr(k), _ptr(v),
+                                       _ptr(gate), _ptr(out), int(pos), _stream()))
+    return out
+
+
+def attn_prefill(cache, layer: int, q, k, v, past_pos: int, gate=None, out=None) -> torch.Tensor:
+    """Causal batched prefill of n = q.shape[0] tokens ([n, H, D])."""
+    n = q.numel() // (cache.num_q_heads * cache.head_dim)
+    out = _check_qgo(cache, q, gate, out, n)
+    _check_kv_rows(cache, k, v, n)
+    _lib.check(_lib.lib().mi_attn_prefill(cache._h, cache.slot(layer), _ptr(q), _ptr(k),
+                                          _ptr(v), _ptr(gate), _ptr(out), int(past_pos), n,
+                                          _stream()))
+    return out
+
+
+def attn_verify(cache, layer: int, q, k, v, past_pos: int, gate=None, out=None) -> torch.Tensor:
+    """K-token speculative verify: same contract as attn_prefill, split-K
+    kernel (HBM-bound) for small K."""
+    n = q.numel() // (cache.num_q_heads * cache.head_dim)
+    out = _check_qgo(cache, q, gate, out, n)
+    _check_kv_rows(cache, k, v, n)
+    _lib.check(_lib.lib().mi_attn_verify(cache._h, cache.slot(layer), _ptr(q), _ptr(k),
+                                         _ptr(v), _ptr(gate), _ptr(out), int(past_pos), n,
+                                         _stream()))
+    return out
+
+
+def kv_pack_v(rows: torch.Tensor, num_kv_heads: int, out: torch.Tensor | None = None,
+              row0: int = 0) -> torch.Tensor:
+    """Token-major V rows [n, G*D] -> the device 8-row block layout."""
+    G, D = num_kv_heads, HEAD_DIM
+    n = rows.numel() // (G * D)
+    if out is None:
+        nblk = (row0 + n + KV_VBLOCK - 1) // KV_VBLOCK
+        out = torch.zeros(nblk * KV_VBLOCK * G * D, dtype=torch.float16, device=rows.device)
+    _check_tensor("rows", rows, n * G * D)
+    if out.numel() < ((row0 + n + KV_VBLOCK - 1) // KV_VBLOCK) * KV_VBLOCK * G * D:
+        raise ValueError("out too small for the packed blocks")
+    if row0 % KV_VBLOCK:
+        raise ValueError("row0 must be a multiple of 8")
+    _lib.check(_lib.lib().mi_kv_pack_v(_ptr(rows), _ptr(out), int(row0), n, G, D, _stream()))
+    return out
+
+
+def ragged_workspace(batch: int, max_len: int, num_q_heads: int = 16, num_kv_heads: int = 2,
+                     device="cuda") -> torch.Tensor:
+    nbytes = _lib.lib().mi_attn_ragged_workspace_size(batch, max_len, num_q_heads,
+                                                      num_kv_heads, HEAD_DIM)
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def attn_decode_ragged(k_rows: torch.Tensor, v_blocks: torch.Tensor, offsets: torch.Tensor,
+                       lengths: torch.Tensor, q: torch.Tensor, max_len: int,
+                       num_kv_heads: int = 2, gate=None, out=None,
+                       workspace: torch.Tensor | None = None,
+                       validate: bool = True) -> torch.Tensor:
+    """Ragged batch: sequence s uses rows [offsets[s], offsets[s]+lengths[s])
+    of k_rows (token-major [rows, G*D]) and v_blocks (8-row block layout,
+    see kv_pack_v).  q: [batch, H, D].  offsets must be multiples of 8."""
+    batch = offsets.numel()
+    G, D = num_kv_heads, HEAD_DIM
+    H = q.numel() // (batch * D)
+    for name, t in (("offsets", offsets), ("lengths", lengths)):
+        _check_tensor(name, t, batch, dtype=torch.int32)
+    _check_tensor("q", q, batch * H * D)
+    if gate is not None:
+        _check_tensor("gate", gate, batch * H * D)
+    if out is None:
+        out = torch.empty_like(q)
+    _check_tensor("out", out, batch * H * D)
+    rows = k_rows.numel() // (G * D)
+    _check_tensor("k_rows", k_rows, rows * G * D)
+    nblk = (rows + KV_VBLOCK - 1) // KV_VBLOCK
+    if v_blocks.numel() < nblk * KV_VBLOCK * G * D:
+        raise ValueError("v_blocks holds fewer blocks than k_rows has rows")
+    if validate:  # host copy of the table (synchronises): bounds the kernel's reads
+        off = offsets.cpu().tolist()
+        ln = lengths.cpu().tolist()
+        for s_, (o, n_) in enumerate(zip(off, ln)):
+            if o < 0 or o % KV_VBLOCK or n_ < 0 or n_ > max_len or o + n_ > rows:
+                raise ValueError(f"sequence {s_}: offset {o}, length {n_} invalid for "
+                                 f"{rows} rows, max_len {max_len}")
+    if workspace is None:
+        workspace = ragged_workspace(batch, max_len, H, G, q.device)
+    _lib.check(_lib.lib().mi_attn_decode_ragged(
+        _ptr(k_rows), _ptr(v_blocks), _ptr(offsets), _ptr(lengths), batch, int(max_len), H, G,
+        D, _ptr(q), _ptr(gate), _ptr(out), _ptr(workspace), workspace.numel(), _stream()))
+    return out

@@ -1,0 +1,71 @@
+// Shared definitions of the gfx950 attention library: vector types, MFMA
+// wrappers, the error channel behind mi_last_error(), and the internal
+// layout of an mi_kv handle.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <vector>
+
+#include "mi_attn.h"
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+namespace mi {
+
+constexpr int kHeadDim = 256;  // Qwen3.6 full-attention head_dim
+constexpr int kGroup = 8;      // query heads per KV head (16 / 2)
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Records `msg` as this thread's last error and returns `st`.
+mi_status fail(mi_status st, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Maps a HIP error to MI_ERR_HIP (or MI_ERR_OOM) with context; MI_OK on success.
+mi_status hip_status(hipError_t e, const char* what);
+void clear_error();
+
+// Checks the head shape the kernels are built for.
+mi_status check_shape(int32_t H, int32_t G, int32_t D);
+
+// Event pair around one launch when profiling is on (mi_prof_enable).
+void prof_begin(const char* name, hipStream_t s);
+void prof_end(const char* name, hipStream_t s);
+
+}  // namespace mi
+
+#define MI_HIP(call)                                        \
+  do {                                                      \
+    hipError_t e_ = (call);                                 \
+    if (e_ != hipSuccess) return mi::hip_status(e_, #call); \
+  } while (0)
+
+#define MI_TRY(call)                 \
+  do {                               \
+    mi_status s_ = (call);           \
+    if (s_ != MI_OK) return s_;      \
+  } while (0)
+
+// Internal state of an mi_kv handle (opaque to callers).
+struct mi_kv {
+  int32_t layers = 0, H = 0, G = 0, D = 0;
+  int64_t cap = 0;  // rows, multiple of MI_KV_CAP_ALIGN
+  int64_t pos = 0;  // Cache::pos
+  std::vector<int64_t> len;        // FullState::len per layer
+  std::vector<_Float16*> k, v;     // device buffers, cap*G*D halves each
+  int device = 0;
+  // Split-K decode / verify partials, grown on demand and kept for reuse.
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+};
+
+namespace mi {
+// Ensures the handle's workspace holds at least `bytes` (synchronous grow).
+mi_status kv_workspace(mi_kv* kv, size_t bytes, void** ws);
+// Enqueues the row copy of kv_cache_append_n on `stream` (no len update).
+mi_status kv_append_rows(mi_kv* kv, int32_t layer, const _Float16* k,
+                         const _Float16* v, int64_t pos, int32_t n,
+                         hipStream_t stream);
+}  // namespace mi

@@ -1,0 +1,519 @@
+// Split-K flash-decoding over the f16 KV cache, for one query token (decode),
+// a few query tokens with a causal tail (speculative verify), or a ragged
+// batch of independent sequences.
+//
+// Reference semantics: attention_scores/softmax/values_batched and
+// sigmoid_gate_inplace (src/math_util.rs:264-269, 323-383); the split-K
+// kernels attn_sdpa_block / attn_sdpa_reduce (src/engine/shaders.metal:
+// 1559-1776) dispatched by encode_pre_expert_full (src/engine/qwen35_moe/
+// fused_exp2.rs:683-719); the causal bound of attn_sdpa_causal_n
+// (shaders.metal:2675-2676: query i sees rows [0, past_pos + i]).
+//
+// Design (gfx950, wave64):
+//  * One workgroup = one (sequence, KV head, chunk of keys).  The eight query
+//    heads of the GQA group — times the query tokens for verify — are the
+//    columns of one MFMA tile, so each K/V byte is read from HBM once per
+//    group rather than once per query head.
+//  * S^T = K . Q^T with v_mfma_f32_16x16x32_f16: K rows are the A operand,
+//    loaded straight from HBM as 128-bit vectors (each lane streams 128
+//    contiguous bytes of one key row); Q^T stays in registers.
+//  * O^T += V^T . P^T with the same instruction: the V cache is stored in
+//    8-row transposed blocks, so the A operand (eight keys of one value
+//    column) is one 128-bit load, and the P^T operand is the S^T
+//    accumulator of the same lane (the QK row order is chosen so that it
+//    is) — no LDS transpose, no shuffles of P.
+//  * Online softmax in base 2 per column; the column max / sum reductions
+//    are two cross-lane xor steps (lanes 16 and 32 apart).
+//  * The waves of a workgroup merge their (m, l, O) through LDS and write one
+//    partial per chunk; attn_combine_kernel merges the chunks, normalises,
+//    applies the sigmoid gate and writes f16.
+#include <cstdlib>
+
+#include "common.h"
+
+namespace {
+
+constexpr int D = mi::kHeadDim;
+constexpr float kNegBig = -1e30f;
+
+struct SplitArgs {
+  const _Float16* k;        // K token-major, row r at k + r*G*D
+  const _Float16* v;        // V blocks, (r,h,i) at v + ((r/8)*G + h)*D*8 + i*8 + r%8
+  const int32_t* offsets;   // ragged: first row of sequence s (else null)
+  const int32_t* lengths;   // ragged: rows of sequence s (else null)
+  int64_t kv_len;           // non-ragged: rows the launch may read
+  int64_t lim0;             // non-ragged: rows visible to query token 0
+  const _Float16* q;        // [batch][nq][H][D]
+  float* part_o;            // [batch][G][max_chunks][ncols][D]
+  float* part_ml;           // [batch][G][max_chunks][ncols][2]
+  int G, H, nq, chunk, max_chunks;
+  float scale_log2e;
+};
+
+__device__ __forceinline__ float xor_max(float x, int mask) {
+  return fmaxf(x, __shfl_xor(x, mask, 64));
+}
+__device__ __forceinline__ float xor_sum(float x, int mask) {
+  return x + __shfl_xor(x, mask, 64);
+}
+
+// NW waves per workgroup; NCB column blocks of 16 columns
+// (column c = token (c / 8), query head in group (c % 8)).
+template <int NW, int NCB>
+__global__ void __launch_bounds__(NW * 64)
+attn_split_kernel(SplitArgs a) {
+  extern __shared__ float smem[];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int g = lane >> 4;   // lane group: k-slot group of the MFMA operands
+  const int j = lane & 15;   // column within a column block / A-operand row
+  const int chunk_idx = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int s = blockIdx.z;
+  const int G = a.G;
+  const int ncols = a.nq * 8;
+
+  int64_t len, row0, lim0;
+  if (a.lengths) {
+    len = a.lengths[s];
+    row0 = a.offsets[s];
+    lim0 = len;
+    // invalid descriptors are reported as NaN by the combine kernel
+    if (len < 0 || len > a.kv_len || row0 < 0 || (row0 & 7)) return;
+  } else {
+    len = a.kv_len;
+    row0 = 0;
+    lim0 = a.lim0;
+  }
+  const int64_t key_begin = (int64_t)chunk_idx * a.chunk;
+  if (key_begin >= len) return;  // uniform over the workgroup
+  const int64_t key_end = min(key_begin + (int64_t)a.chunk, len);
+  const int64_t rstride = (int64_t)G * D;
+
+  // Q^T operand: lane (g, j) holds q[token][head][64g + 8kk + 0..7] for its
+  // column j, kk = 0..7.  Padding columns are zero and fully masked.
+  f16x8 qf[NCB][8];
+  int64_t lim[NCB];
+#pragma unroll
+  for (int cb = 0; cb < NCB; cb++) {
+    const int c = cb * 16 + j;
+    const int tok = c >> 3;
+    if (c < ncols) {
+      const _Float16* qp =
+          a.q + (((int64_t)s * a.nq + tok) * a.H + kvh * 8 + (c & 7)) * D + 64 * g;
+#pragma unroll
+      for (int kk = 0; kk < 8; kk++) qf[cb][kk] = *(const f16x8*)(qp + 8 * kk);
+      lim[cb] = lim0 + tok;
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < 8; kk++) qf[cb][kk] = f16x8{};
+      lim[cb] = 0;
+    }
+  }
+
+  float m[NCB], l[NCB];
+  f32x4 acc[NCB][16];
+#pragma unroll
+  for (int cb = 0; cb < NCB; cb++) {
+    m[cb] = kNegBig;
+    l[cb] = 0.f;
+#pragma unroll
+    for (int d = 0; d < 16; d++) acc[cb][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const _Float16* kbase = a.k + row0 * rstride + kvh * D + 64 * g;
+  for (int64_t k0 = key_begin + 32 * w; k0 < key_end; k0 += 32 * NW) {
+    // K operand rows: tile u, A-row j <-> key k0 + 8*(j/4) + 4u + j%4, so that
+    // accumulator row 4g+e of tile u is key k0 + 8g + 4u + e.
+    f16x8 kf[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const int64_t key = k0 + 8 * (j >> 2) + 4 * u + (j & 3);
+      if (key < key_end) {
+        const _Float16* kp = kbase + key * rstride;
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) kf[u][kk] = *(const f16x8*)(kp + 8 * kk);
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) kf[u][kk] = f16x8{};
+      }
+    }
+    // V operand: lane (g, j), value block dblk holds V^T[dblk*16 + j][keys
+    // k0+8g .. k0+8g+7] = one 16-byte vector of the block layout.
+    f16x8 vf[16];
+    const int64_t vkey = k0 + 8 * g;
+    if (vkey < key_end) {
+      const _Float16* vp =
+          a.v + (((row0 + vkey) >> 3) * G + kvh) * (int64_t)(D * 8) + j * 8;
+#pragma unroll
+      for (int dblk = 0; dblk < 16; dblk++) vf[dblk] = *(const f16x8*)(vp + dblk * 128);
+      if (vkey + 8 > key_end) {  // tail: rows past the end may be stale or NaN
+        const int valid = (int)(key_end - vkey);
+#pragma unroll
+        for (int dblk = 0; dblk < 16; dblk++)
+#pragma unroll
+          for (int e = 0; e < 8; e++)
+            if (e >= valid) vf[dblk][e] = (_Float16)0.f;
+      }
+    } else {
+#pragma unroll
+      for (int dblk = 0; dblk < 16; dblk++) vf[dblk] = f16x8{};
+    }
+
+#pragma unroll
+    for (int cb = 0; cb < NCB; cb++) {
+      f32x4 st[2];
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        f32x4 c4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++)
+          c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[u][kk], qf[cb][kk], c4, 0, 0, 0);
+        st[u] = c4;
+      }
+      // scale into base 2 and mask keys outside this column's window
+      float mt = kNegBig;
+#pragma unroll
+      for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int64_t key = k0 + 8 * g + 4 * u + e;
+          float x = st[u][e] * a.scale_log2e;
+          x = (key < lim[cb] && key < key_end) ? x : -INFINITY;
+          st[u][e] = x;
+          mt = fmaxf(mt, x);
+        }
+      mt = xor_max(mt, 16);
+      mt = xor_max(mt, 32);
+      const float mnew = fmaxf(m[cb], mt);
+      const float alpha = exp2f(m[cb] - mnew);
+      float rs = 0.f;
+      f16x8 pf;
+#pragma unroll
+      for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float p = exp2f(st[u][e] - mnew);
+          rs += p;
+          pf[4 * u + e] = (_Float16)p;
+        }
+      rs = xor_sum(rs, 16);
+      rs = xor_sum(rs, 32);
+      l[cb] = l[cb] * alpha + rs;
+      m[cb] = mnew;
+#pragma unroll
+      for (int dblk = 0; dblk < 16; dblk++) {
+        acc[cb][dblk] *= alpha;
+        acc[cb][dblk] =
+            __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dblk], pf, acc[cb][dblk], 0, 0, 0);
+      }
+    }
+  }
+
+  // ---- merge the NW waves through LDS: [NW][ncols][D] O, [NW][ncols] m, l
+  float* so = smem;
+  float* sm = smem + NW * ncols * D;
+  float* sl = sm + NW * ncols;
+#pragma unroll
+  for (int cb = 0; cb < NCB; cb++) {
+    const int c = cb * 16 + j;
+    if (c < ncols) {
+      float* dst = so + ((int64_t)w * ncols + c) * D + 4 * g;
+#pragma unroll
+      for (int dblk = 0; dblk < 16; dblk++) *(f32x4*)(dst + dblk * 16) = acc[cb][dblk];
+      if (g == 0) {
+        sm[w * ncols + c] = m[cb];
+        sl[w * ncols + c] = l[cb];
+      }
+    }
+  }
+  __syncthreads();
+  const int64_t pbase = (((int64_t)s * G + kvh) * a.max_chunks + chunk_idx) * ncols;
+  for (int idx = threadIdx.x; idx < ncols * D; idx += NW * 64) {
+    const int c = idx / D;
+    const int d = idx % D;
+    float M = kNegBig;
+#pragma unroll
+    for (int ww = 0; ww < NW; ww++) M = fmaxf(M, sm[ww * ncols + c]);
+    float o = 0.f, L = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ww++) {
+      const float sc = exp2f(sm[ww * ncols + c] - M);
+      o += so[((int64_t)ww * ncols + c) * D + d] * sc;
+      L += sl[ww * ncols + c] * sc;
+    }
+    a.part_o[(pbase + c) * D + d] = o;
+    if (d == 0) {
+      a.part_ml[(pbase + c) * 2 + 0] = M;
+      a.part_ml[(pbase + c) * 2 + 1] = L;
+    }
+  }
+}
+
+struct CombineArgs {
+  const int32_t* offsets;  // ragged (else null)
+  const int32_t* lengths;  // ragged (else null)
+  int64_t kv_len;          // rows (ragged: max_len)
+  const float* part_o;
+  const float* part_ml;
+  const _Float16* gate;    // [batch][nq][H][D] or null
+  _Float16* out;           // [batch][nq][H][D]
+  int G, H, nq, chunk, max_chunks;
+};
+
+// One workgroup per (column, KV head, sequence); one thread per output
+// element of the head.  out = sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M),
+// zero when the denominator is zero (the reference's `sum > 0` guard and
+// zero-filled output, math_util.rs:357, 372), then * sigmoid(gate).
+__global__ void __launch_bounds__(256)
+attn_combine_kernel(CombineArgs a) {
+  const int c = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int s = blockIdx.z;
+  const int ncols = a.nq * 8;
+  int64_t len = a.kv_len;
+  bool bad = false;
+  if (a.lengths) {
+    len = a.lengths[s];
+    const int32_t off = a.offsets[s];
+    bad = len < 0 || len > a.kv_len || off < 0 || (off & 7);
+    if (bad) len = 0;
+  }
+  const int nch = (int)((len + a.chunk - 1) / a.chunk);
+  const int64_t pbase = ((int64_t)s * a.G + kvh) * a.max_chunks;
+  float M = kNegBig;
+  for (int ch = 0; ch < nch; ch++) M = fmaxf(M, a.part_ml[((pbase + ch) * ncols + c) * 2]);
+  const int tok = c >> 3;
+  const int hq = kvh * 8 + (c & 7);
+  const int64_t obase = (((int64_t)s * a.nq + tok) * a.H + hq) * D;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float o = 0.f, L = 0.f;
+    for (int ch = 0; ch < nch; ch++) {
+      const int64_t pi = (pbase + ch) * ncols + c;
+      const float sc = exp2f(a.part_ml[pi * 2] - M);
+      L += a.part_ml[pi * 2 + 1] * sc;
+      o += a.part_o[pi * D + d] * sc;
+    }
+    float r = (L > 0.f) ? o / L : 0.f;
+    if (bad) r = __builtin_nanf("");
+    if (a.gate) {
+      const float gv = (float)a.gate[obase + d];
+      r *= 1.f / (1.f + expf(-gv));
+    }
+    a.out[obase + d] = (_Float16)r;
+  }
+}
+
+int env_int(const char* name, int dflt) {
+  const char* e = getenv(name);
+  return (e && *e) ? atoi(e) : dflt;
+}
+
+// Keys per workgroup.  Target about two workgroups per CU (256 CUs) over the
+// whole launch, never less than one 32-key tile per wave.
+int pick_chunk(int nw, int64_t max_len, int64_t units) {
+  int forced = env_int("MI_ATTN_SPLIT_CHUNK", 0);
+  if (forced > 0) return (forced + 32 * nw - 1) / (32 * nw) * (32 * nw);
+  const int64_t step = 32 * nw;
+  int64_t target_wgs = 512;
+  int64_t chunks_per_unit = (target_wgs + units - 1) / units;
+  int64_t chunk = (max_len + chunks_per_unit - 1) / chunks_per_unit;
+  chunk = (chunk + step - 1) / step * step;
+  if (chunk < step) chunk = step;
+  return (int)chunk;
+}
+
+struct SplitPlan {
+  int nw, chunk, max_chunks;
+};
+
+// Wave count and chunking of one split launch.  More than two query tokens
+// need 32 merge columns, which fit the 160 KB of LDS only with 4 waves.
+SplitPlan plan_split(int64_t max_len, int64_t units, int nq) {
+  SplitPlan p;
+  p.nw = (nq > 2 || env_int("MI_ATTN_SPLIT_WAVES", 8) == 4) ? 4 : 8;
+  p.chunk = pick_chunk(p.nw, max_len, units);
+  p.max_chunks = (int)((max_len + p.chunk - 1) / p.chunk);
+  if (p.max_chunks < 1) p.max_chunks = 1;
+  return p;
+}
+
+template <int NW, int NCB>
+mi_status launch_split(const SplitArgs& a, int64_t batch, hipStream_t stream) {
+  const size_t lds = ((size_t)NW * a.nq * 8 * (D + 2)) * sizeof(float);
+  static bool attr_done = false;
+  if (!attr_done) {
+    MI_HIP(hipFuncSetAttribute((const void*)attn_split_kernel<NW, NCB>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    attr_done = true;
+  }
+  dim3 grid(a.max_chunks, a.G, (unsigned)batch);
+  mi::prof_begin("attn_split", stream);
+  attn_split_kernel<NW, NCB><<<grid, NW * 64, lds, stream>>>(a);
+  mi::prof_end("attn_split", stream);
+  MI_HIP(hipGetLastError());
+  return MI_OK;
+}
+
+size_t split_workspace_bytes(int64_t batch, int G, int max_chunks, int nq) {
+  size_t units = (size_t)batch * G * max_chunks * nq * 8;
+  return units * (D + 2) * sizeof(float) + 256;
+}
+
+// Runs split + combine for nq <= 4 query tokens per sequence.
+mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets,
+                    const int32_t* lengths, int64_t kv_len, int64_t lim0,
+                    int64_t max_len, int64_t batch, int H, int G, int nq,
+                    const _Float16* q, const _Float16* gate, _Float16* out,
+                    void* ws, size_t ws_bytes, hipStream_t stream) {
+  const SplitPlan plan = plan_split(max_len, batch * G, nq);
+  const int nw = plan.nw;
+  SplitArgs a;
+  a.k = k;
+  a.v = v;
+  a.offsets = offsets;
+  a.lengths = lengths;
+  a.kv_len = kv_len;
+  a.lim0 = lim0;
+  a.q = q;
+  a.G = G;
+  a.H = H;
+  a.nq = nq;
+  a.chunk = plan.chunk;
+  a.max_chunks = plan.max_chunks;
+  a.scale_log2e = mi::kLog2e / sqrtf((float)D);
+  const size_t need = split_workspace_bytes(batch, G, a.max_chunks, nq);
+  if (ws_bytes < need)
+    return mi::fail(MI_ERR_INVALID_ARG, "workspace %zu bytes < %zu needed", ws_bytes, need);
+  a.part_o = (float*)ws;
+  a.part_ml = a.part_o + (size_t)batch * G * a.max_chunks * nq * 8 * D;
+  mi_status st;
+  if (nq <= 2) {
+    st = (nw == 8) ? launch_split<8, 1>(a, batch, stream) : launch_split<4, 1>(a, batch, stream);
+  } else {
+    st = launch_split<4, 2>(a, batch, stream);  // plan_split forces 4 waves here
+  }
+  MI_TRY(st);
+  CombineArgs c;
+  c.offsets = offsets;
+  c.lengths = lengths;
+  c.kv_len = kv_len;
+  c.part_o = a.part_o;
+  c.part_ml = a.part_ml;
+  c.gate = gate;
+  c.out = out;
+  c.G = G;
+  c.H = H;
+  c.nq = nq;
+  c.chunk = a.chunk;
+  c.max_chunks = a.max_chunks;
+  dim3 grid(nq * 8, G, (unsigned)batch);
+  mi::prof_begin("attn_combine", stream);
+  attn_combine_kernel<<<grid, 256, 0, stream>>>(c);
+  mi::prof_end("attn_combine", stream);
+  MI_HIP(hipGetLastError());
+  return MI_OK;
+}
+
+mi_status check_layer(const mi_kv* kv, int32_t layer) {
+  if (!kv) return mi::fail(MI_ERR_INVALID_ARG, "null mi_kv handle");
+  if (layer < 0 || layer >= kv->layers)
+    return mi::fail(MI_ERR_INVALID_ARG, "layer %d out of [0, %d)", layer, kv->layers);
+  return MI_OK;
+}
+
+// Verify / decode over the cache: n query tokens at positions past_pos ..
+// past_pos+n-1, rows [0, past_pos+n) already in the cache.
+mi_status cache_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float16* gate,
+                       _Float16* out, int64_t past_pos, int32_t n, hipStream_t stream) {
+  const int64_t lim0 = past_pos + 1;
+  for (int32_t t0 = 0; t0 < n; t0 += 4) {
+    const int nq = (n - t0) < 4 ? (n - t0) : 4;
+    const int64_t rows = past_pos + t0 + nq;  // rows the last token of this group sees
+    const SplitPlan plan = plan_split(rows, kv->G, nq);
+    void* ws;
+    MI_TRY(mi::kv_workspace(kv, split_workspace_bytes(1, kv->G, plan.max_chunks, nq), &ws));
+    const int64_t qoff = (int64_t)t0 * kv->H * D;
+    MI_TRY(run_split(kv->k[layer], kv->v[layer], nullptr, nullptr, rows, lim0 + t0,
+                     rows, 1, kv->H, kv->G, nq, q + qoff, gate ? gate + qoff : nullptr,
+                     out + qoff, ws, kv->ws_bytes, stream));
+  }
+  return MI_OK;
+}
+
+}  // namespace
+
+namespace mi {
+mi_status attend_cache(mi_kv* kv, int32_t layer, const _Float16* q, const _Float16* gate,
+                       _Float16* out, int64_t past_pos, int32_t n, hipStream_t stream) {
+  return cache_attend(kv, layer, q, gate, out, past_pos, n, stream);
+}
+}  // namespace mi
+
+extern "C" mi_status mi_attn_decode(mi_kv* kv, int32_t layer, const mi_f16* q,
+                                    const mi_f16* gate, mi_f16* out, int64_t seq_len,
+                                    mi_stream stream) {
+  mi::clear_error();
+  MI_TRY(check_layer(kv, layer));
+  if (!q || !out) return mi::fail(MI_ERR_INVALID_ARG, "null q/out");
+  if (seq_len < 0 || seq_len > kv->cap)
+    return mi::fail(MI_ERR_OUT_OF_RANGE, "seq_len %lld outside [0, capacity %lld]",
+                    (long long)seq_len, (long long)kv->cap);
+  // seq_len == 0 runs no split work; the combine writes zeros (times the gate).
+  return cache_attend(kv, layer, (const _Float16*)q, (const _Float16*)gate, (_Float16*)out,
+                      seq_len - 1, 1, (hipStream_t)stream);
+}
+
+extern "C" mi_status mi_attn_step(mi_kv* kv, int32_t layer, const mi_f16* q,
+                                  const mi_f16* k, const mi_f16* v, const mi_f16* gate,
+                                  mi_f16* out, int64_t pos, mi_stream stream) {
+  mi::clear_error();
+  MI_TRY(check_layer(kv, layer));
+  if (!q || !k || !v || !out) return mi::fail(MI_ERR_INVALID_ARG, "null q/k/v/out");
+  MI_TRY(mi_kv_append(kv, layer, k, v, pos, 1, stream));
+  return cache_attend(kv, layer, (const _Float16*)q, (const _Float16*)gate, (_Float16*)out,
+                      pos, 1, (hipStream_t)stream);
+}
+
+extern "C" mi_status mi_attn_verify(mi_kv* kv, int32_t layer, const mi_f16* q,
+                                    const mi_f16* k, const mi_f16* v, const mi_f16* gate,
+                                    mi_f16* out, int64_t past_pos, int32_t n,
+                                    mi_stream stream) {
+  mi::clear_error();
+  MI_TRY(check_layer(kv, layer));
+  if (!q || !k || !v || !out) return mi::fail(MI_ERR_INVALID_ARG, "null q/k/v/out");
+  if (n <= 0) return mi::fail(MI_ERR_INVALID_ARG, "n=%d", n);
+  MI_TRY(mi_kv_append(kv, layer, k, v, past_pos, n, stream));
+  return cache_attend(kv, layer, (const _Float16*)q, (const _Float16*)gate, (_Float16*)out,
+                      past_pos, n, (hipStream_t)stream);
+}
+
+extern "C" size_t mi_attn_ragged_workspace_size(int32_t batch, int32_t max_len,
+                                                int32_t num_q_heads, int32_t num_kv_heads,
+                                                int32_t head_dim) {
+  if (batch <= 0 || max_len <= 0 || num_kv_heads <= 0) return 256;
+  (void)num_q_heads;
+  (void)head_dim;
+  const SplitPlan plan = plan_split(max_len, (int64_t)batch * num_kv_heads, 1);
+  return split_workspace_bytes(batch, num_kv_heads, plan.max_chunks, 1);
+}
+
+extern "C" mi_status mi_attn_decode_ragged(const mi_f16* k_rows, const mi_f16* v_rows,
+                                           const int32_t* offsets, const int32_t* lengths,
+                                           int32_t batch, int32_t max_len,
+                                           int32_t num_q_heads, int32_t num_kv_heads,
+                                           int32_t head_dim, const mi_f16* q,
+                                           const mi_f16* gate, mi_f16* out, void* workspace,
+                                           size_t workspace_bytes, mi_stream stream) {
+  mi::clear_error();
+  MI_TRY(mi::check_shape(num_q_heads, num_kv_heads, head_dim));
+  if (!k_rows || !v_rows || !offsets || !lengths || !q || !out || !workspace)
+    return mi::fail(MI_ERR_INVALID_ARG, "null pointer argument");
+  if (batch <= 0 || max_len < 0)
+    return mi::fail(MI_ERR_INVALID_ARG, "batch=%d max_len=%d", batch, max_len);
+  const int64_t ml = max_len > 0 ? max_len : 1;
+  return run_split((const _Float16*)k_rows, (const _Float16*)v_rows, offsets, lengths, ml, 0,
+                   ml, batch, num_q_heads, num_kv_heads, 1, (const _Float16*)q,
+                   (const _Float16*)gate, (_Float16*)out, workspace, workspace_bytes,
+                   (hipStream_t)stream);
+}

@@ -1,0 +1,454 @@
+// KV-cache state of the full-attention layers: allocation and doubling
+// growth, position-only rollback, append kernels, host transfer, and the
+// error channel of the whole library.
+//
+// Reference semantics: src/cache.rs (Cache::new :45-76, reset :84-94,
+// set_pos :102-109, copy_from :112-128, FullState :273-287), the GPU KV
+// buffers of src/engine/qwen35_moe/metal_context.rs (:316-319, growth
+// :368-431, upload/download :804-882) and the append kernels
+// kv_cache_append / kv_cache_append_n (src/engine/shaders.metal:2370-2383,
+// 2774-2792).
+//
+// Device layout (per layer): K token-major [cap][G*D]; V in 8-row transposed
+// blocks [cap/8][G][D][8], so one 16-byte load returns the eight keys of one
+// value column — the operand order the decode and prefill MFMA kernels
+// consume without an LDS transpose.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "common.h"
+
+namespace {
+thread_local char g_err[512] = "";
+}
+
+namespace mi {
+
+mi_status fail(mi_status st, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return st;
+}
+
+mi_status hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return MI_OK;
+  mi_status st = (e == hipErrorOutOfMemory) ? MI_ERR_OOM : MI_ERR_HIP;
+  return fail(st, "%s failed: %s", what, hipGetErrorString(e));
+}
+
+void clear_error() { g_err[0] = 0; }
+
+mi_status check_shape(int32_t H, int32_t G, int32_t D) {
+  if (H <= 0 || G <= 0 || D <= 0 || H % G != 0)
+    return fail(MI_ERR_INVALID_ARG, "bad head shape H=%d G=%d D=%d", H, G, D);
+  if (D != kHeadDim || H / G != kGroup)
+    return fail(MI_ERR_UNSUPPORTED,
+                "kernels are built for head_dim=%d and %d query heads per KV "
+                "head; got head_dim=%d, H/G=%d",
+                kHeadDim, kGroup, D, H / G);
+  return MI_OK;
+}
+
+}  // namespace mi
+
+extern "C" const char* mi_last_error(void) { return g_err; }
+
+extern "C" const char* mi_version(void) { return "mi_attn 0.1 gfx950"; }
+
+extern "C" void mi_roofline_peaks(double* hbm_gbps, double* f16_tflops) {
+  if (hbm_gbps) *hbm_gbps = MI_PEAK_HBM_GBPS;
+  if (f16_tflops) *f16_tflops = MI_PEAK_F16_TFLOPS;
+}
+
+// ------------------------------------------------------------- kernels ----
+
+// K rows: straight 16-byte copies of rows [pos, pos+n).
+__global__ void __launch_bounds__(256)
+kv_append_k_kernel(const f16x8* __restrict__ src, f16x8* __restrict__ dst,
+                   int64_t pos, int64_t n, int64_t vec_per_row) {
+  int64_t total = n * vec_per_row;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    dst[pos * vec_per_row + i] = src[i];
+  }
+}
+
+// V rows into the 8-row transposed block layout.  One thread owns
+// (block b, KV head h, 8 consecutive columns d0..d0+7): it gathers those
+// columns of the block's rows that lie in [pos, pos+n) and writes them
+// either as eight 16-byte column vectors (whole block covered) or element
+// by element (first/last partial block; rows outside the range keep their
+// contents).  src is token-major [n][G*D].
+__global__ void __launch_bounds__(256)
+kv_pack_v_kernel(const _Float16* __restrict__ src, _Float16* __restrict__ vblk,
+                 int64_t pos, int64_t n, int G, int D) {
+  const int64_t b_first = pos / MI_KV_VBLOCK;
+  const int64_t b_last = (pos + n - 1) / MI_KV_VBLOCK;
+  const int cvec = D / 8;
+  const int64_t total = (b_last - b_first + 1) * G * cvec;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = b_first + idx / (G * cvec);
+    const int h = (int)((idx / cvec) % G);
+    const int d0 = (int)(idx % cvec) * 8;
+    const int64_t r0 = b * MI_KV_VBLOCK;
+    _Float16* blk = vblk + ((b * G + h) * (int64_t)D + d0) * MI_KV_VBLOCK;
+    if (r0 >= pos && r0 + MI_KV_VBLOCK <= pos + n) {
+      f16x8 rowv[8];
+#pragma unroll
+      for (int rr = 0; rr < 8; rr++)
+        rowv[rr] = *(const f16x8*)(src + (r0 + rr - pos) * G * D + h * D + d0);
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        f16x8 col;
+#pragma unroll
+        for (int rr = 0; rr < 8; rr++) col[rr] = rowv[rr][i];
+        *(f16x8*)(blk + i * MI_KV_VBLOCK) = col;
+      }
+    } else {
+      for (int rr = 0; rr < 8; rr++) {
+        int64_t r = r0 + rr;
+        if (r < pos || r >= pos + n) continue;
+        f16x8 row = *(const f16x8*)(src + (r - pos) * G * D + h * D + d0);
+#pragma unroll
+        for (int i = 0; i < 8; i++) blk[i * MI_KV_VBLOCK + rr] = row[i];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------- host helpers --
+
+namespace {
+
+int64_t round_cap(int64_t rows) {
+  if (rows < MI_KV_CAP_ALIGN) rows = MI_KV_CAP_ALIGN;
+  return (rows + MI_KV_CAP_ALIGN - 1) / MI_KV_CAP_ALIGN * MI_KV_CAP_ALIGN;
+}
+
+size_t layer_bytes(const mi_kv* kv, int64_t cap) {
+  return (size_t)cap * kv->G * kv->D * sizeof(_Float16);
+}
+
+mi_status check_layer(const mi_kv* kv, int32_t layer) {
+  if (!kv) return mi::fail(MI_ERR_INVALID_ARG, "null mi_kv handle");
+  if (layer < 0 || layer >= kv->layers)
+    return mi::fail(MI_ERR_INVALID_ARG, "layer %d out of [0, %d)", layer, kv->layers);
+  return MI_OK;
+}
+
+void free_layers(mi_kv* kv) {
+  for (auto p : kv->k) if (p) (void)hipFree(p);
+  for (auto p : kv->v) if (p) (void)hipFree(p);
+  kv->k.clear();
+  kv->v.clear();
+}
+
+// Allocates `cap`-row buffers for every layer, copies the first
+// `keep_rows` rows of the old buffers (all of them: rows past len are stale
+// but must survive, as the reference's whole-buffer regrow keeps them) and
+// zero-fills the rest.
+mi_status realloc_layers(mi_kv* kv, int64_t cap, int64_t keep_rows) {
+  std::vector<_Float16*> nk(kv->layers, nullptr), nv(kv->layers, nullptr);
+  size_t bytes = layer_bytes(kv, cap);
+  size_t keep = layer_bytes(kv, keep_rows);
+  for (int l = 0; l < kv->layers; l++) {
+    hipError_t e1 = hipMalloc((void**)&nk[l], bytes);
+    hipError_t e2 = (e1 == hipSuccess) ? hipMalloc((void**)&nv[l], bytes) : e1;
+    if (e2 != hipSuccess) {
+      for (auto p : nk) if (p) (void)hipFree(p);
+      for (auto p : nv) if (p) (void)hipFree(p);
+      return mi::hip_status(e2, "hipMalloc(kv cache)");
+    }
+    if (keep) {
+      MI_HIP(hipMemcpy(nk[l], kv->k[l], keep, hipMemcpyDeviceToDevice));
+      MI_HIP(hipMemcpy(nv[l], kv->v[l], keep, hipMemcpyDeviceToDevice));
+    }
+    MI_HIP(hipMemset((char*)nk[l] + keep, 0, bytes - keep));
+    MI_HIP(hipMemset((char*)nv[l] + keep, 0, bytes - keep));
+  }
+  MI_HIP(hipDeviceSynchronize());
+  free_layers(kv);
+  kv->k = nk;
+  kv->v = nv;
+  kv->cap = cap;
+  return MI_OK;
+}
+
+}  // namespace
+
+namespace mi {
+
+mi_status kv_workspace(mi_kv* kv, size_t bytes, void** ws) {
+  if (bytes > kv->ws_bytes) {
+    if (kv->ws) {
+      MI_HIP(hipDeviceSynchronize());
+      (void)hipFree(kv->ws);
+      kv->ws = nullptr;
+      kv->ws_bytes = 0;
+    }
+    size_t b = bytes + bytes / 4;
+    MI_HIP(hipMalloc(&kv->ws, b));
+    kv->ws_bytes = b;
+  }
+  *ws = kv->ws;
+  return MI_OK;
+}
+
+mi_status kv_append_rows(mi_kv* kv, int32_t layer, const _Float16* k,
+                         const _Float16* v, int64_t pos, int32_t n,
+                         hipStream_t stream) {
+  const int64_t vec_per_row = (int64_t)kv->G * kv->D / 8;
+  int64_t kvec = (int64_t)n * vec_per_row;
+  int kgrid = (int)std::min<int64_t>((kvec + 255) / 256, 4096);
+  mi::prof_begin("kv_append", stream);
+  kv_append_k_kernel<<<kgrid, 256, 0, stream>>>((const f16x8*)k, (f16x8*)kv->k[layer],
+                                                pos, n, vec_per_row);
+  MI_HIP(hipGetLastError());
+  int64_t nblk = (pos + n - 1) / MI_KV_VBLOCK - pos / MI_KV_VBLOCK + 1;
+  int64_t vthreads = nblk * kv->G * (kv->D / 8);
+  int vgrid = (int)std::min<int64_t>((vthreads + 255) / 256, 4096);
+  kv_pack_v_kernel<<<vgrid, 256, 0, stream>>>(v, kv->v[layer], pos, n, kv->G, kv->D);
+  mi::prof_end("kv_append", stream);
+  MI_HIP(hipGetLastError());
+  return MI_OK;
+}
+
+}  // namespace mi
+
+// ------------------------------------------------------------- C ABI ------
+
+extern "C" mi_status mi_kv_create(int32_t num_layers, int32_t num_q_heads,
+                                  int32_t num_kv_heads, int32_t head_dim,
+                                  int64_t capacity, mi_kv** out) {
+  mi::clear_error();
+  if (!out) return mi::fail(MI_ERR_INVALID_ARG, "null output pointer");
+  *out = nullptr;
+  if (num_layers <= 0) return mi::fail(MI_ERR_INVALID_ARG, "num_layers=%d", num_layers);
+  if (capacity < 0) return mi::fail(MI_ERR_INVALID_ARG, "capacity=%lld", (long long)capacity);
+  MI_TRY(mi::check_shape(num_q_heads, num_kv_heads, head_dim));
+  mi_kv* kv = new mi_kv();
+  kv->layers = num_layers;
+  kv->H = num_q_heads;
+  kv->G = num_kv_heads;
+  kv->D = head_dim;
+  kv->len.assign(num_layers, 0);
+  (void)hipGetDevice(&kv->device);
+  mi_status st = realloc_layers(kv, round_cap(capacity), 0);
+  if (st != MI_OK) {
+    delete kv;
+    return st;
+  }
+  *out = kv;
+  return MI_OK;
+}
+
+extern "C" void mi_kv_destroy(mi_kv* kv) {
+  if (!kv) return;
+  (void)hipDeviceSynchronize();
+  free_layers(kv);
+  if (kv->ws) (void)hipFree(kv->ws);
+  delete kv;
+}
+
+extern "C" mi_status mi_kv_reserve(mi_kv* kv, int64_t capacity) {
+  mi::clear_error();
+  if (!kv) return mi::fail(MI_ERR_INVALID_ARG, "null mi_kv handle");
+  if (capacity <= kv->cap) return MI_OK;
+  // Doubling growth (metal_context.rs:368-431), at least to `capacity`.
+  int64_t cap = kv->cap;
+  while (cap < capacity) cap *= 2;
+  return realloc_layers(kv, round_cap(cap), kv->cap);
+}
+
+extern "C" mi_status mi_kv_capacity(const mi_kv* kv, int64_t* capacity) {
+  if (!kv || !capacity) return mi::fail(MI_ERR_INVALID_ARG, "null argument");
+  *capacity = kv->cap;
+  return MI_OK;
+}
+
+extern "C" mi_status mi_kv_shape(const mi_kv* kv, int32_t* num_layers,
+                                 int32_t* num_q_heads, int32_t* num_kv_heads,
+                                 int32_t* head_dim) {
+  if (!kv) return mi::fail(MI_ERR_INVALID_ARG, "null mi_kv handle");
+  if (num_layers) *num_layers = kv->layers;
+  if (num_q_heads) *num_q_heads = kv->H;
+  if (num_kv_heads) *num_kv_heads = kv->G;
+  if (head_dim) *head_dim = kv->D;
+  return MI_OK;
+}
+
+extern "C" mi_status mi_kv_set_pos(mi_kv* kv, int64_t pos) {
+  mi::clear_error();
+  if (!kv) return mi::fail(MI_ERR_INVALID_ARG, "null mi_kv handle");
+  if (pos < 0 || pos > kv->cap)
+    return mi::fail(MI_ERR_OUT_OF_RANGE, "pos %lld outside [0, capacity %lld]",
+                    (long long)pos, (long long)kv->cap);
+  kv->pos = pos;
+  for (auto& l : kv->len) l = pos;
+  return MI_OK;
+}
+
+extern "C" mi_status mi_kv_reset(mi_kv* kv) { return mi_kv_set_pos(kv, 0); }
+
+extern "C" mi_status mi_kv_pos(const mi_kv* kv, int64_t* pos) {
+  if (!kv || !pos) return mi::fail(MI_ERR_INVALID_ARG, "null argument");
+  *pos = kv->pos;
+  return MI_OK;
+}
+
+extern "C" mi_status mi_kv_len(const mi_kv* kv, int32_t layer, int64_t* len) {
+  MI_TRY(check_layer(kv, layer));
+  if (!len) return mi::fail(MI_ERR_INVALID_ARG, "null argument");
+  *len = kv->len[layer];
+  return MI_OK;
+}
+
+extern "C" mi_status mi_kv_set_len(mi_kv* kv, int32_t layer, int64_t len) {
+  MI_TRY(check_layer(kv, layer));
+  if (len < 0 || len > kv->cap)
+    return mi::fail(MI_ERR_OUT_OF_RANGE, "len %lld outside [0, capacity %lld]",
+                    (long long)len, (long long)kv->cap);
+  kv->len[layer] = len;
+  return MI_OK;
+}
+
+extern "C" mi_status mi_kv_layer_ptrs(mi_kv* kv, int32_t layer, mi_f16** k,
+                                      mi_f16** v) {
+  MI_TRY(check_layer(kv, layer));
+  if (k) *k = (mi_f16*)kv->k[layer];
+  if (v) *v = (mi_f16*)kv->v[layer];
+  return MI_OK;
+}
+
+extern "C" mi_status mi_kv_append(mi_kv* kv, int32_t layer, const mi_f16* k,
+                                  const mi_f16* v, int64_t pos, int32_t n,
+                                  mi_stream stream) {
+  mi::clear_error();
+  MI_TRY(check_layer(kv, layer));
+  if (!k || !v) return mi::fail(MI_ERR_INVALID_ARG, "null k/v");
+  if (n <= 0) return mi::fail(MI_ERR_INVALID_ARG, "n=%d", n);
+  if (pos < 0) return mi::fail(MI_ERR_OUT_OF_RANGE, "pos=%lld", (long long)pos);
+  if (pos + n > kv->cap) MI_TRY(mi_kv_reserve(kv, pos + n));
+  MI_TRY(mi::kv_append_rows(kv, layer, (const _Float16*)k, (const _Float16*)v, pos, n,
+                            (hipStream_t)stream));
+  kv->len[layer] = pos + n;
+  return MI_OK;
+}
+
+extern "C" mi_status mi_kv_pack_v(const mi_f16* src_rows, mi_f16* dst_v,
+                                  int64_t row0, int64_t rows,
+                                  int32_t num_kv_heads, int32_t head_dim,
+                                  mi_stream stream) {
+  mi::clear_error();
+  if (!src_rows || !dst_v) return mi::fail(MI_ERR_INVALID_ARG, "null pointer");
+  if (rows <= 0 || row0 < 0 || num_kv_heads <= 0 || head_dim <= 0 || head_dim % 8)
+    return mi::fail(MI_ERR_INVALID_ARG, "bad pack arguments");
+  int64_t nblk = (row0 + rows - 1) / MI_KV_VBLOCK - row0 / MI_KV_VBLOCK + 1;
+  int64_t threads = nblk * num_kv_heads * (head_dim / 8);
+  int grid = (int)std::min<int64_t>((threads + 255) / 256, 4096);
+  kv_pack_v_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(
+      (const _Float16*)src_rows, (_Float16*)dst_v, row0, rows, num_kv_heads, head_dim);
+  MI_HIP(hipGetLastError());
+  return MI_OK;
+}
+
+namespace {
+
+// Host copy of the V blocks covering rows [row0, row0+rows).
+mi_status download_v_blocks(const mi_kv* kv, int32_t layer, int64_t row0, int64_t rows,
+                            std::vector<_Float16>& blocks, int64_t* b0) {
+  *b0 = row0 / MI_KV_VBLOCK;
+  int64_t b1 = (row0 + rows - 1) / MI_KV_VBLOCK;
+  size_t per_block = (size_t)kv->G * kv->D * MI_KV_VBLOCK;
+  blocks.resize((size_t)(b1 - *b0 + 1) * per_block);
+  MI_HIP(hipMemcpy(blocks.data(), kv->v[layer] + *b0 * per_block,
+                   blocks.size() * sizeof(_Float16), hipMemcpyDeviceToHost));
+  return MI_OK;
+}
+
+mi_status check_rows(const mi_kv* kv, int64_t row0, int64_t rows) {
+  if (row0 < 0 || rows < 0 || row0 + rows > kv->cap)
+    return mi::fail(MI_ERR_OUT_OF_RANGE, "rows [%lld, %lld) outside capacity %lld",
+                    (long long)row0, (long long)(row0 + rows), (long long)kv->cap);
+  return MI_OK;
+}
+
+}  // namespace
+
+extern "C" mi_status mi_kv_upload(mi_kv* kv, int32_t layer, const mi_f16* host_k,
+                                  const mi_f16* host_v, int64_t row0, int64_t rows) {
+  mi::clear_error();
+  MI_TRY(check_layer(kv, layer));
+  if (!host_k || !host_v) return mi::fail(MI_ERR_INVALID_ARG, "null host buffer");
+  MI_TRY(check_rows(kv, row0, rows));
+  if (rows == 0) return MI_OK;
+  MI_HIP(hipDeviceSynchronize());
+  const int64_t rl = (int64_t)kv->G * kv->D;
+  MI_HIP(hipMemcpy(kv->k[layer] + row0 * rl, host_k, (size_t)(rows * rl) * 2,
+                   hipMemcpyHostToDevice));
+  std::vector<_Float16> blocks;
+  int64_t b0;
+  MI_TRY(download_v_blocks(kv, layer, row0, rows, blocks, &b0));
+  const _Float16* src = (const _Float16*)host_v;
+  for (int64_t r = row0; r < row0 + rows; r++) {
+    int64_t b = r / MI_KV_VBLOCK - b0;
+    int rr = (int)(r % MI_KV_VBLOCK);
+    for (int h = 0; h < kv->G; h++)
+      for (int i = 0; i < kv->D; i++)
+        blocks[((b * kv->G + h) * kv->D + i) * MI_KV_VBLOCK + rr] =
+            src[(r - row0) * rl + h * kv->D + i];
+  }
+  size_t per_block = (size_t)kv->G * kv->D * MI_KV_VBLOCK;
+  MI_HIP(hipMemcpy(kv->v[layer] + b0 * per_block, blocks.data(),
+                   blocks.size() * sizeof(_Float16), hipMemcpyHostToDevice));
+  return MI_OK;
+}
+
+extern "C" mi_status mi_kv_download(const mi_kv* kv, int32_t layer, mi_f16* host_k,
+                                    mi_f16* host_v, int64_t row0, int64_t rows) {
+  mi::clear_error();
+  MI_TRY(check_layer(kv, layer));
+  if (!host_k || !host_v) return mi::fail(MI_ERR_INVALID_ARG, "null host buffer");
+  MI_TRY(check_rows(kv, row0, rows));
+  if (rows == 0) return MI_OK;
+  MI_HIP(hipDeviceSynchronize());
+  const int64_t rl = (int64_t)kv->G * kv->D;
+  MI_HIP(hipMemcpy(host_k, kv->k[layer] + row0 * rl, (size_t)(rows * rl) * 2,
+                   hipMemcpyDeviceToHost));
+  std::vector<_Float16> blocks;
+  int64_t b0;
+  MI_TRY(download_v_blocks(kv, layer, row0, rows, blocks, &b0));
+  _Float16* dst = (_Float16*)host_v;
+  for (int64_t r = row0; r < row0 + rows; r++) {
+    int64_t b = r / MI_KV_VBLOCK - b0;
+    int rr = (int)(r % MI_KV_VBLOCK);
+    for (int h = 0; h < kv->G; h++)
+      for (int i = 0; i < kv->D; i++)
+        dst[(r - row0) * rl + h * kv->D + i] =
+            blocks[((b * kv->G + h) * kv->D + i) * MI_KV_VBLOCK + rr];
+  }
+  return MI_OK;
+}
+
+extern "C" mi_status mi_kv_copy_from(mi_kv* dst, const mi_kv* src) {
+  mi::clear_error();
+  if (!dst || !src) return mi::fail(MI_ERR_INVALID_ARG, "null mi_kv handle");
+  if (dst->layers != src->layers || dst->H != src->H || dst->G != src->G || dst->D != src->D)
+    return mi::fail(MI_ERR_INVALID_ARG, "cache shape mismatch");
+  if (dst == src) return MI_OK;
+  if (dst->cap < src->cap) MI_TRY(realloc_layers(dst, src->cap, 0));
+  MI_HIP(hipDeviceSynchronize());
+  size_t bytes = layer_bytes(src, src->cap);
+  for (int l = 0; l < src->layers; l++) {
+    MI_HIP(hipMemcpy(dst->k[l], src->k[l], bytes, hipMemcpyDeviceToDevice));
+    MI_HIP(hipMemcpy(dst->v[l], src->v[l], bytes, hipMemcpyDeviceToDevice));
+  }
+  MI_HIP(hipDeviceSynchronize());
+  dst->pos = src->pos;
+  dst->len = src->len;
+  return MI_OK;
+}

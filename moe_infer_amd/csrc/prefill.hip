@@ -1,0 +1,267 @@
+// Causal batched prefill: flash-attention forward on gfx950 MFMA.
+//
+// Reference semantics: op1_full_batched (src/engine/qwen35_moe/batched.rs:
+// 233-260): kv_cache_append_n of the n new rows at past_pos, then
+// attn_sdpa_causal_n (src/engine/shaders.metal:2656-2769) where query i
+// attends rows [0, past_pos + i] inclusive, then sigmoid_gate per token.
+//
+// Design:
+//  * Workgroup = 4 waves = 128 queries of one query head; wave w owns 32
+//    queries.  Grid order is heaviest query tile first, and the eight heads
+//    of a GQA group on the same query tile are placed on one XCD so that
+//    their identical K/V tile reads share that XCD's L2.
+//  * K/V tiles of 64 keys are staged in LDS (double-buffered, one barrier per
+//    tile); global loads of tile t+1 are in flight while tile t computes.
+//  * S^T = K . Q^T with v_mfma_f32_32x32x16_f16 (A = K rows from LDS,
+//    B = Q^T held in registers for the whole kernel); the online softmax is
+//    per lane column (one query per lane column), so row statistics need a
+//    single cross-lane step (lanes 32 apart).
+//  * O^T += V^T . P^T: the V tile is kept in the cache's 8-row transposed
+//    block layout, so the A operand is one 128-bit LDS read, and the QK row
+//    order is chosen so that P^T is the lane's own S^T accumulator.
+//  * Epilogue: divide by the row sum, multiply by sigmoid(gate), write f16.
+#include "common.h"
+
+namespace {
+
+constexpr int D = mi::kHeadDim;
+constexpr int BQ = 128;        // queries per workgroup
+constexpr int BK = 64;         // keys per LDS tile
+constexpr int KROW = D + 8;    // padded K row in LDS (halves): 528 bytes
+constexpr int K_TILE_HALVES = BK * KROW;
+constexpr int V_TILE_HALVES = BK * D;  // 8 blocks of [D][8]
+constexpr int STAGE_HALVES = K_TILE_HALVES + V_TILE_HALVES;
+constexpr float kNegBig = -1e30f;
+
+struct PrefillArgs {
+  const _Float16* q;      // [n][H][D]
+  const _Float16* k;      // cache K, token-major [cap][G*D]
+  const _Float16* v;      // cache V blocks
+  const _Float16* gate;   // [n][H][D] or null
+  _Float16* out;          // [n][H][D]
+  int64_t past;           // past_pos
+  int n, H, G, ntiles, work;
+  float scale_log2e;
+};
+
+// Row m of a 32-key QK tile holds key swap_bits_2_3(m): then accumulator
+// element e of lane half hl (row 8*(e/4) + 4*hl + e%4) is key
+// 16*(e/8) + 8*hl + e%8, i.e. the PV step e/8 sees eight consecutive keys
+// per lane half — one V block.
+__device__ __forceinline__ int qk_row_key(int m) {
+  return (m & 0x13) | ((m & 4) << 1) | ((m & 8) >> 1);
+}
+
+__global__ void __launch_bounds__(256, 1)
+attn_prefill_kernel(PrefillArgs a) {
+  extern __shared__ _Float16 lds[];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int hl = lane >> 5;   // lane half
+  const int col = lane & 31;  // query column of this lane
+
+  // blockIdx -> (query tile, KV head, head in group); 8 heads of one
+  // (tile, KV head) land on one XCD (dispatch is round-robin over 8 XCDs).
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7, r = bid >> 3;
+  const int li = (r >> 3) * 64 + xcd * 8 + (r & 7);
+  if (li >= a.work) return;
+  const int hg = li & 7;
+  const int kvh = (li >> 3) % a.G;
+  const int tile_rank = (li >> 3) / a.G;
+  const int qtile = a.ntiles - 1 - tile_rank;  // heaviest first
+  const int hq = kvh * 8 + hg;
+  const int q0 = qtile * BQ;
+  const int64_t G_D = (int64_t)a.G * D;
+
+  // Q^T operand for this lane's query: 16 k-steps of 8 halves.
+  const int qi = q0 + 32 * w + col;
+  f16x8 qf[16];
+  if (qi < a.n) {
+    const _Float16* qp = a.q + ((int64_t)qi * a.H + hq) * D + 8 * hl;
+#pragma unroll
+    for (int ks = 0; ks < 16; ks++) qf[ks] = *(const f16x8*)(qp + 16 * ks);
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < 16; ks++) qf[ks] = f16x8{};
+  }
+  const int64_t qpos = a.past + qi;                     // this lane's query position
+  const int64_t wave_first = a.past + q0 + 32 * w;       // smallest query position of the wave
+  const int64_t wave_last = wave_first + 31;
+  const int64_t kv_len = a.past + a.n;
+  int64_t kv_end = a.past + q0 + BQ;
+  if (kv_end > kv_len) kv_end = kv_len;
+  const int nt = (int)((kv_end + BK - 1) / BK);
+
+  f32x16 acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) acc[i] = f32x16{};
+  float m = kNegBig, l = 0.f;
+
+  // Global -> register staging of one tile: 8 K chunks + 8 V chunks / thread.
+  f16x8 kreg[8], vreg[8];
+  auto load_tile = [&](int t) {
+    const int64_t key0 = (int64_t)t * BK;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int c = threadIdx.x + 256 * i;   // 0..2047
+      const int row = c >> 5, ch = c & 31;   // K: row, 16-byte chunk
+      kreg[i] = *(const f16x8*)(a.k + (key0 + row) * G_D + kvh * D + ch * 8);
+      const int blk = c >> 8, d = c & 255;   // V: block, column
+      const int64_t gb = (key0 >> 3) + blk;
+      f16x8 vv = *(const f16x8*)(a.v + ((gb * a.G + kvh) * D + d) * 8);
+      const int64_t valid = kv_len - gb * 8;  // rows past the end may hold stale data
+      if (valid < 8) {
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+          if (e >= valid) vv[e] = (_Float16)0.f;
+      }
+      vreg[i] = vv;
+    }
+  };
+  auto store_tile = [&](int buf) {
+    _Float16* ks = lds + buf * STAGE_HALVES;
+    _Float16* vs = ks + K_TILE_HALVES;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int c = threadIdx.x + 256 * i;
+      *(f16x8*)(ks + (c >> 5) * KROW + (c & 31) * 8) = kreg[i];
+      *(f16x8*)(vs + c * 8) = vreg[i];
+    }
+  };
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  for (int t = 0; t < nt; t++) {
+    const int buf = t & 1;
+    if (t + 1 < nt) load_tile(t + 1);
+    const int64_t key0 = (int64_t)t * BK;
+    if (key0 <= wave_last) {
+      const _Float16* ks = lds + buf * STAGE_HALVES;
+      const _Float16* vs = ks + K_TILE_HALVES;
+      f32x16 st[2];
+#pragma unroll
+      for (int sub = 0; sub < 2; sub++) {
+        const _Float16* kr = ks + (sub * 32 + qk_row_key(col)) * KROW + 8 * hl;
+        f32x16 c16 = f32x16{};
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+          c16 = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8*)(kr + 16 * k), qf[k],
+                                                       c16, 0, 0, 0);
+        st[sub] = c16;
+      }
+      const bool need_mask = key0 + BK - 1 > wave_first;
+      float mt = kNegBig;
+#pragma unroll
+      for (int sub = 0; sub < 2; sub++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          float x = st[sub][e] * a.scale_log2e;
+          if (need_mask) {
+            const int64_t key = key0 + sub * 32 + 16 * (e >> 3) + 8 * hl + (e & 7);
+            x = (key <= qpos) ? x : -INFINITY;
+          }
+          st[sub][e] = x;
+          mt = fmaxf(mt, x);
+        }
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      const float mnew = fmaxf(m, mt);
+      const float alpha = exp2f(m - mnew);
+      m = mnew;
+      float rs = 0.f;
+      f16x8 pf[2][2];
+#pragma unroll
+      for (int sub = 0; sub < 2; sub++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const float p = exp2f(st[sub][e] - mnew);
+          rs += p;
+          pf[sub][e >> 3][e & 7] = (_Float16)p;
+        }
+      rs += __shfl_xor(rs, 32, 64);
+      l = l * alpha + rs;
+#pragma unroll
+      for (int i = 0; i < 8; i++) acc[i] *= alpha;
+#pragma unroll
+      for (int sub = 0; sub < 2; sub++)
+#pragma unroll
+        for (int stp = 0; stp < 2; stp++) {
+          // V block of keys sub*32 + 16*stp + 8*hl .. +7
+          const _Float16* vb = vs + (sub * 4 + 2 * stp + hl) * (D * 8) + col * 8;
+#pragma unroll
+          for (int i = 0; i < 8; i++)
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                *(const f16x8*)(vb + i * 32 * 8), pf[sub][stp], acc[i], 0, 0, 0);
+        }
+    }
+    if (t + 1 < nt) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (qi >= a.n) return;
+  const float inv = (l > 0.f) ? 1.f / l : 0.f;
+  const int64_t obase = ((int64_t)qi * a.H + hq) * D;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+#pragma unroll
+    for (int e4 = 0; e4 < 4; e4++) {
+      const int d = i * 32 + 8 * e4 + 4 * hl;
+      f16x4 o;
+      f16x4 gv = a.gate ? *(const f16x4*)(a.gate + obase + d) : f16x4{};
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        float x = acc[i][4 * e4 + e] * inv;
+        if (a.gate) x *= 1.f / (1.f + expf(-(float)gv[e]));
+        o[e] = (_Float16)x;
+      }
+      *(f16x4*)(a.out + obase + d) = o;
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
+                                     const mi_f16* k, const mi_f16* v, const mi_f16* gate,
+                                     mi_f16* out, int64_t past_pos, int32_t n,
+                                     mi_stream stream) {
+  mi::clear_error();
+  if (!kv) return mi::fail(MI_ERR_INVALID_ARG, "null mi_kv handle");
+  if (layer < 0 || layer >= kv->layers)
+    return mi::fail(MI_ERR_INVALID_ARG, "layer %d out of [0, %d)", layer, kv->layers);
+  if (!q || !k || !v || !out) return mi::fail(MI_ERR_INVALID_ARG, "null q/k/v/out");
+  if (n <= 0) return mi::fail(MI_ERR_INVALID_ARG, "n=%d", n);
+  if (past_pos < 0) return mi::fail(MI_ERR_OUT_OF_RANGE, "past_pos=%lld", (long long)past_pos);
+  // Tiles read up to 64 rows past the last key; capacity is a multiple of 256
+  // rows, so it suffices that the rows themselves fit.
+  MI_TRY(mi_kv_append(kv, layer, k, v, past_pos, n, stream));
+  hipStream_t s = (hipStream_t)stream;
+  PrefillArgs a;
+  a.q = (const _Float16*)q;
+  a.k = kv->k[layer];
+  a.v = kv->v[layer];
+  a.gate = (const _Float16*)gate;
+  a.out = (_Float16*)out;
+  a.past = past_pos;
+  a.n = n;
+  a.H = kv->H;
+  a.G = kv->G;
+  a.ntiles = (n + BQ - 1) / BQ;
+  a.work = a.ntiles * kv->G * 8;
+  a.scale_log2e = mi::kLog2e / sqrtf((float)D);
+  static bool attr_done = false;
+  const size_t lds = 2 * STAGE_HALVES * sizeof(_Float16);
+  if (!attr_done) {
+    MI_HIP(hipFuncSetAttribute((const void*)attn_prefill_kernel,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    attr_done = true;
+  }
+  const int grid = (a.work + 63) / 64 * 64;
+  mi::prof_begin("attn_prefill", s);
+  attn_prefill_kernel<<<grid, 256, lds, s>>>(a);
+  mi::prof_end("attn_prefill", s);
+  MI_HIP(hipGetLastError());
+  return MI_OK;
+}

@@ -1,0 +1,143 @@
+"""The engine's full-attention step over a device KV cache, with the
+reference Engine's method names for the attention / cache subset
+(src/python_bindings.rs:104-318, trait Engine in src/engine.rs:32-93).
+
+What the reference's Engine does around attention (embedding, projections,
+norms, RoPE, MoE, lm_head) is outside this library; callers hand in the
+per-layer q / k / v / gate projections and get the gated attention output.
+
+  forward(layers)            one token through every full-attention layer:
+                             append at engine_pos, attend [0, pos], gate;
+                             then pos += 1 (fused_exp2.rs:989-1039)
+  forward_batched(layers)    n tokens per layer, causal (batched.rs:129-312);
+                             pos += n (fused_exp3.rs:291)
+  mtp_forward(...)           MTP layer: append at mtp_pos, attend, mtp_pos += 1
+                             (mtp.rs:143-156, 223)
+  mtp_verify(...)            K draft tokens at once (split-K verify kernel)
+  mtp_reset / mtp_rollback   MtpState::reset / rollback (mtp.rs:39-47)
+  snapshot_state / restore_snapshot   positions only: KV rows past the restored
+                             position stay but are never read (fused_exp3.rs:321-365)
+  telemetry()                per-call wall times when recording is on
+                             (record_engine_telemetry, engine.rs:13-24)
+"""
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass
+
+import torch
+
+from . import attention
+from .kv_cache import Cache
+
+_RECORD_TELEMETRY = False
+
+
+def record_engine_telemetry(on: bool) -> None:
+    global _RECORD_TELEMETRY
+    _RECORD_TELEMETRY = bool(on)
+
+
+@dataclass(frozen=True)
+class EngineSnapshot:
+    pos: int
+    mtp_pos: int
+
+
+class Engine:
+    def __init__(self, cache: Cache, mtp_capacity: int = 4096):
+        self.cache = cache
+        self.mtp_cache = Cache(num_layers=1, num_q_heads=cache.num_q_heads,
+                               num_kv_heads=cache.num_kv_heads, head_dim=cache.head_dim,
+                               capacity=mtp_capacity)
+        self._telemetry: dict[str, list[float] | float] = {}
+
+    # -- positions -----------------------------------------------------------
+    def engine_pos(self) -> int:
+        return self.cache.pos
+
+    @property
+    def mtp_pos(self) -> int:
+        return self.mtp_cache.pos
+
+    def _record(self, key: str, t0: float) -> None:
+        if _RECORD_TELEMETRY:
+            torch.cuda.synchronize()
+            self._telemetry.setdefault(key, []).append((time.perf_counter() - t0) * 1e3)
+
+    # -- main model ------------------------------------------------------------
+    def forward(self, layers):
+        """layers: sequence of (layer, q[H*D], k[G*D], v[G*D], gate|None).
+        Returns the gated attention outputs, one per entry."""
+        t0 = time.perf_counter()
+        pos = self.cache.pos
+        outs = [attention.attn_step(self.cache, layer, q, k, v, pos, gate=gate)
+                for layer, q, k, v, gate in layers]
+        self.cache.set_pos(pos + 1)
+        self.cache.gpu_dirty = True
+        self._record("engine.full_attention_ms", t0)
+        return outs
+
+    def forward_batched(self, layers):
+        """layers: sequence of (layer, q[n,H,D], k[n,G*D], v[n,G*D], gate|None);
+        n == 1 falls back to the token-serial step (fused_exp3.rs:169-171)."""
+        t0 = time.perf_counter()
+        pos = self.cache.pos
+        outs, n = [], None
+        for layer, q, k, v, gate in layers:
+            n_l = q.numel() // (self.cache.num_q_heads * self.cache.head_dim)
+            if n is not None and n_l != n:
+                raise ValueError("every layer must carry the same token count")
+            n = n_l
+            if n == 1:
+                outs.append(attention.attn_step(self.cache, layer, q, k, v, pos, gate=gate))
+            else:
+                outs.append(attention.attn_prefill(self.cache, layer, q, k, v, pos, gate=gate))
+        if n is not None:
+            self.cache.set_pos(pos + n)
+            self.cache.gpu_dirty = True
+        self._record("engine.full_attention_batched_ms", t0)
+        return outs
+
+    # -- MTP draft head ----------------------------------------------------------
+    def mtp_forward(self, q, k, v, gate=None):
+        pos = self.mtp_cache.pos
+        out = attention.attn_step(self.mtp_cache, 0, q, k, v, pos, gate=gate)
+        self.mtp_cache.set_pos(pos + 1)
+        return out
+
+    def mtp_verify(self, q, k, v, gate=None):
+        """K tokens appended at mtp_pos; query i attends [0, mtp_pos + i]."""
+        pos = self.mtp_cache.pos
+        n = q.numel() // (self.mtp_cache.num_q_heads * self.mtp_cache.head_dim)
+        out = attention.attn_verify(self.mtp_cache, 0, q, k, v, pos, gate=gate)
+        self.mtp_cache.set_pos(pos + n)
+        return out
+
+    def mtp_reset(self) -> None:
+        self.mtp_cache.set_pos(0)
+
+    def mtp_rollback(self, pos: int) -> None:
+        self.mtp_cache.set_pos(pos)
+
+    # -- speculative-decoding rollback ------------------------------------------------
+    def snapshot_state(self) -> EngineSnapshot:
+        return EngineSnapshot(self.cache.pos, self.mtp_cache.pos)
+
+    def restore_snapshot(self, snap: EngineSnapshot) -> None:
+        self.cache.set_pos(snap.pos)
+        self.mtp_cache.set_pos(snap.mtp_pos)
+
+    # -- cache transfer (the cache already lives on the device) -----------------------
+    def upload_cache(self, cache: Cache) -> None:
+        if cache is not self.cache:
+            self.cache.copy_from(cache)
+        cache.cpu_dirty = False
+
+    def download_cache(self, cache: Cache) -> None:
+        if cache is not self.cache:
+            cache.copy_from(self.cache)
+        cache.gpu_dirty = False
+
+    def telemetry(self) -> dict:
+        return dict(self._telemetry)

@@ -1,0 +1,137 @@
+"""Decode, engine step and K-token verify on the GPU against the CPU oracle
+(reference f32 math of src/math_util.rs:264-269, 323-383 on the same f16
+inputs), through the C ABI."""
+import numpy as np
+import pytest
+import torch
+
+from moe_infer_amd import Cache, attn_decode, attn_step, attn_verify
+from oracle import oracle as O
+
+from .conftest import f16
+from .gpu_util import announce, assert_close, dev
+
+pytestmark = pytest.mark.gpu
+H, G, D = 16, 2, 256
+
+
+def filled_cache(k, v, capacity=None):
+    L = k.shape[0]
+    c = Cache(num_layers=1, capacity=capacity or max(L, 1))
+    if L:
+        c.upload(0, k, v)
+        c.set_pos(L)
+    return c
+
+
+@pytest.mark.parametrize("L", [1, 2, 7, 31, 32, 33, 255, 256, 257, 512, 1000, 4099])
+@pytest.mark.parametrize("gated", [False, True])
+def test_decode_matches_oracle(L, gated):
+    announce(f"decode L={L} gated={gated}")
+    rng = np.random.default_rng(100 + L)
+    q, k, v, g = f16(rng, H * D), f16(rng, L, G * D), f16(rng, L, G * D), f16(rng, H * D)
+    c = filled_cache(k, v)
+    out = attn_decode(c, 0, dev(q), L, gate=dev(g) if gated else None)
+    ref = O.decode(q, k, v, L, gate=g if gated else None)
+    assert_close(out, ref, f"decode L={L}")
+
+
+def test_decode_ctx32k_matches_oracle():
+    """batch 1, context 32768, seed 2."""
+    announce("decode C2 L=32768")
+    L = 32768
+    rng = np.random.default_rng(2)
+    q, k, v = f16(rng, H * D), f16(rng, L, G * D), f16(rng, L, G * D)
+    c = filled_cache(k, v)
+    out = attn_decode(c, 0, dev(q), L)
+    assert_close(out, O.decode(q, k, v, L), "decode L=32768 vs f32 oracle")
+    assert_close(out, O.decode_f64(q, k, v, L), "decode L=32768 vs f64 oracle")
+
+
+def test_decode_seq_len_zero_and_bounds():
+    announce("decode L=0 / bounds")
+    rng = np.random.default_rng(5)
+    c = filled_cache(f16(rng, 8, G * D), f16(rng, 8, G * D))
+    q = dev(f16(rng, H * D))
+    out = attn_decode(c, 0, q, 0)
+    assert torch.count_nonzero(out).item() == 0
+    with pytest.raises(ValueError):
+        attn_decode(c, 0, q, c.capacity + 1)
+
+
+def test_decode_never_reads_rows_past_seq_len():
+    """Rows past seq_len (stale after rollback) are never read: poison them
+    with NaN/inf and the output must equal the oracle on the valid rows."""
+    announce("decode poisoned tail")
+    rng = np.random.default_rng(6)
+    L, P = 45, 300
+    k, v, q = f16(rng, P, G * D), f16(rng, P, G * D), f16(rng, H * D)
+    k[L:] = np.float16(np.nan)
+    v[L:] = np.float16(np.inf)
+    c = filled_cache(k, v)
+    out = attn_decode(c, 0, dev(q), L)
+    assert_close(out, O.decode(q, k[:L], v[:L], L), "decode poisoned tail")
+
+
+def test_engine_step_sequence():
+    """append-then-attend token by token (cpu.rs:141-167): token t attends
+    rows [0, t] including its own row."""
+    announce("attn_step sequence")
+    rng = np.random.default_rng(9)
+    T = 300
+    c = Cache(num_layers=2, capacity=16)  # 256 rows: grows by doubling at t = 256
+    ks, vs = f16(rng, T, G * D), f16(rng, T, G * D)
+    for t in range(T):
+        q, g = f16(rng, H * D), f16(rng, H * D)
+        for layer in (0, 1):
+            out = attn_step(c, layer, dev(q), dev(ks[t]), dev(vs[t]), t, gate=dev(g))
+            if t % 37 == 0 or t in (255, 256, T - 1):
+                assert_close(out, O.decode(q, ks[:t + 1], vs[:t + 1], t + 1, gate=g),
+                             f"step t={t} layer={layer}")
+        assert c.len(0) == t + 1
+        c.set_pos(t + 1)
+    assert c.capacity >= T
+
+
+@pytest.mark.parametrize("n,past", [(1, 0), (2, 5), (3, 31), (4, 61), (4, 255), (7, 100),
+                                    (9, 1000)])
+def test_verify_matches_causal_oracle(n, past):
+    announce(f"verify n={n} past={past}")
+    rng = np.random.default_rng(1000 * n + past)
+    kp, vp = f16(rng, past, G * D), f16(rng, past, G * D)
+    q, k, v, g = f16(rng, n, H, D), f16(rng, n, G * D), f16(rng, n, G * D), f16(rng, n, H, D)
+    c = filled_cache(kp, vp, capacity=past + n)
+    out = attn_verify(c, 0, dev(q), dev(k), dev(v), past, gate=dev(g))
+    ref = O.causal(q, np.concatenate([kp, k]), np.concatenate([vp, v]), past, gate=g)
+    assert_close(out, ref, f"verify n={n} past={past}")
+    assert c.len(0) == past + n
+
+
+def test_verify_c5_and_rollback():
+    """K=4 drafts appended to a 65536-row cache, causal
+    within the drafts, sigmoid gate; then rollback to 65538: rows below are
+    unchanged, len == 65538, and the next append lands at 65538."""
+    announce("verify C5 65536+4 and rollback")
+    rng = np.random.default_rng(5)
+    P, K = 65536, 4
+    kp, vp = f16(rng, P, G * D), f16(rng, P, G * D)
+    q, k, v, g = f16(rng, K, H, D), f16(rng, K, G * D), f16(rng, K, G * D), f16(rng, K, H, D)
+    c = filled_cache(kp, vp, capacity=P + K)
+    out = attn_verify(c, 0, dev(q), dev(k), dev(v), P, gate=dev(g))
+    kall, vall = np.concatenate([kp, k]), np.concatenate([vp, v])
+    assert_close(out, O.causal(q, kall, vall, P, gate=g), "verify C5")
+    c.set_pos(P + 2)
+    assert c.pos == P + 2 and c.len(0) == P + 2
+    kd, vd = c.download(0, rows=P + K)
+    assert np.array_equal(kd.view(np.uint16), kall.view(np.uint16))
+    assert np.array_equal(vd.view(np.uint16), vall.view(np.uint16))
+    # the accepted prefix decodes like a fresh cache of P+2 rows
+    q2, k2, v2 = f16(rng, H * D), f16(rng, G * D), f16(rng, G * D)
+    out2 = attn_step(c, 0, dev(q2), dev(k2), dev(v2), P + 2)
+    kref = np.concatenate([kall[:P + 2], k2[None]])
+    vref = np.concatenate([vall[:P + 2], v2[None]])
+    assert_close(out2, O.decode(q2, kref, vref, P + 3), "decode after rollback")
+    kd, vd = c.download(0, rows=P + K)
+    assert np.array_equal(kd[P + 2].view(np.uint16), k2.view(np.uint16))
+    assert np.array_equal(kd[P + 3].view(np.uint16), k[3].view(np.uint16))  # stale, untouched
+    assert np.array_equal(vd[:P + 2].view(np.uint16), vall[:P + 2].view(np.uint16))

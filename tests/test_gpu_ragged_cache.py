@@ -1,0 +1,169 @@
+"""Ragged batched decode and the KV-cache state operations on the GPU:
+append / upload / download bit-exactness, position-only rollback, reset,
+doubling growth, copy_from and save/load (src/cache.rs semantics, modelled
+by oracle.CacheModel)."""
+import numpy as np
+import pytest
+import torch
+
+from moe_infer_amd import Cache, attn_decode, attn_decode_ragged, kv_cache_append, kv_pack_v
+from oracle import oracle as O
+
+from .conftest import f16
+from .gpu_util import announce, assert_close, dev, host
+
+pytestmark = pytest.mark.gpu
+H, G, D = 16, 2, 256
+
+
+def ragged_buffers(rng, lengths):
+    offsets, rows = [], 0
+    for n in lengths:
+        offsets.append(rows)
+        rows += (n + 7) // 8 * 8  # sequences start on an 8-row block
+    rows = max(rows, 8)
+    k, v = f16(rng, rows, G * D), f16(rng, rows, G * D)
+    return np.array(offsets, np.int32), k, v
+
+
+@pytest.mark.parametrize("lengths", [[5, 0, 17, 1, 8, 9, 33, 300],
+                                     [1024, 1, 2049, 255, 4096, 0, 777, 129]])
+def test_ragged_matches_oracle(lengths):
+    announce(f"ragged {lengths}")
+    rng = np.random.default_rng(sum(lengths))
+    lengths = np.array(lengths, np.int32)
+    offsets, k, v = ragged_buffers(rng, lengths)
+    b = len(lengths)
+    q, g = f16(rng, b, H, D), f16(rng, b, H, D)
+    vb = kv_pack_v(dev(v), G)
+    out = attn_decode_ragged(dev(k), vb, torch.from_numpy(offsets).cuda(),
+                             torch.from_numpy(lengths).cuda(), dev(q), int(lengths.max()),
+                             gate=dev(g))
+    ref = O.decode_ragged(q, k, v, offsets, lengths, gate=g)
+    assert_close(out, ref, f"ragged {list(lengths)}")
+    o = host(out)
+    assert np.all(o[lengths == 0] == 0)
+
+
+def test_ragged_c3_shape():
+    """64 sequences, lengths U[1024, 32768] (seed 3);
+    8 sequences are checked against the oracle, all 64 against the GPU
+    single-sequence decode of the same rows (ragged == independent decodes)."""
+    announce("ragged C3 64 seqs")
+    rng = np.random.default_rng(3)
+    lengths = rng.integers(1024, 32769, size=64).astype(np.int32)
+    offsets, k, v = ragged_buffers(rng, lengths)
+    q = f16(rng, 64, H, D)
+    out = host(attn_decode_ragged(dev(k), kv_pack_v(dev(v), G), torch.from_numpy(offsets).cuda(),
+                                  torch.from_numpy(lengths).cuda(), dev(q), 32768))
+    for s in range(0, 64, 8):
+        a, n = offsets[s], lengths[s]
+        assert_close(out[s], O.decode(q[s], k[a:a + n], v[a:a + n], n), f"C3 seq {s} (L={n})")
+    c = Cache(num_layers=1, capacity=32768)
+    for s in range(64):
+        a, n = offsets[s], lengths[s]
+        c.upload(0, k[a:a + n], v[a:a + n])
+        dec = host(attn_decode(c, 0, dev(q[s]), int(n)))
+        # different split-K chunking: equal up to f32 re-association
+        assert_close(out[s], dec.reshape(H, D), f"C3 seq {s} vs decode", atol=5e-4)
+
+
+def test_ragged_rejects_bad_tables():
+    rng = np.random.default_rng(0)
+    k, v = f16(rng, 64, G * D), f16(rng, 64, G * D)
+    vb = kv_pack_v(dev(v), G)
+    q = dev(f16(rng, 2, H, D))
+    for off, ln in (([0, 3], [4, 4]), ([0, 8], [4, 100]), ([0, 8], [4, -1])):
+        with pytest.raises(ValueError):
+            attn_decode_ragged(dev(k), vb, torch.tensor(off, dtype=torch.int32).cuda(),
+                               torch.tensor(ln, dtype=torch.int32).cuda(), q, 64)
+
+
+def test_pack_v_layout():
+    """V rows land at ((r/8)*G + h)*D*8 + i*8 + r%8 (the documented layout)."""
+    rng = np.random.default_rng(11)
+    v = f16(rng, 21, G * D)
+    blk = host(kv_pack_v(dev(v), G)).reshape(-1, G, D, 8)
+    for r in range(21):
+        for h in range(G):
+            assert np.array_equal(blk[r // 8, h, :, r % 8].view(np.uint16),
+                                  v[r, h * D:(h + 1) * D].view(np.uint16))
+
+
+def test_append_download_bit_exact_and_rollback():
+    announce("cache append/rollback")
+    rng = np.random.default_rng(12)
+    layers, cap = 3, 64
+    c = Cache(num_layers=layers, capacity=cap)
+    m = O.CacheModel(layers, G * D, c.capacity)
+    pos = 0
+    for step, n in enumerate([1, 3, 8, 13, 1, 40, 7]):
+        for layer in range(layers):
+            k, v = f16(rng, n, G * D), f16(rng, n, G * D)
+            kv_cache_append(c, layer, dev(k), dev(v), pos)
+            m.append(layer, k, v, pos)
+            assert c.len(layer) == m.len[layer]
+        pos += n
+        if step == 3:  # roll back 5 rows: nothing is erased
+            pos -= 5
+            c.set_pos(pos)
+            m.set_pos(pos)
+    torch.cuda.synchronize()
+    for layer in range(layers):
+        kd, vd = c.download(layer, rows=c.capacity)
+        mk, mv = m.k[layer][:c.capacity], m.v[layer][:c.capacity]
+        assert np.array_equal(kd.view(np.uint16), mk.view(np.uint16))
+        assert np.array_equal(vd.view(np.uint16), mv.view(np.uint16))
+    c.reset()
+    assert c.pos == 0 and all(c.len(i) == 0 for i in range(layers))
+    kd, _ = c.download(0, rows=pos)
+    assert np.array_equal(kd.view(np.uint16), m.k[0][:pos].view(np.uint16))  # reset erases nothing
+
+
+def test_upload_unaligned_rows_and_growth():
+    rng = np.random.default_rng(13)
+    c = Cache(num_layers=1, capacity=256)
+    base_k, base_v = f16(rng, 256, G * D), f16(rng, 256, G * D)
+    c.upload(0, base_k, base_v)
+    k, v = f16(rng, 11, G * D), f16(rng, 11, G * D)
+    c.upload(0, k, v, row0=5)  # partial V blocks on both ends
+    ek, ev = base_k.copy(), base_v.copy()
+    ek[5:16], ev[5:16] = k, v
+    kd, vd = c.download(0, rows=256)
+    assert np.array_equal(kd.view(np.uint16), ek.view(np.uint16))
+    assert np.array_equal(vd.view(np.uint16), ev.view(np.uint16))
+    c.set_pos(200)
+    kx, vx = f16(rng, 100, G * D), f16(rng, 100, G * D)
+    kv_cache_append(c, 0, dev(kx), dev(vx), 250)  # grows 256 -> 512, keeps every row
+    assert c.capacity == 512 and c.len(0) == 350
+    kd, vd = c.download(0, rows=350)
+    assert np.array_equal(kd[:250].view(np.uint16), ek[:250].view(np.uint16))
+    assert np.array_equal(vd[:250].view(np.uint16), ev[:250].view(np.uint16))
+    assert np.array_equal(vd[250:].view(np.uint16), vx.view(np.uint16))
+
+
+def test_copy_from_and_save_load(tmp_path):
+    rng = np.random.default_rng(14)
+    cfg = {"num_hidden_layers": 8, "num_attention_heads": 16, "num_key_value_heads": 2,
+           "head_dim": 256, "linear_num_value_heads": 32, "linear_num_key_heads": 16}
+    c = Cache(cfg, capacity=300)
+    assert c.full_layers == [3, 7]
+    with pytest.raises(ValueError):
+        c.slot(2)
+    for layer in c.full_layers:
+        kv_cache_append(c, layer, dev(f16(rng, 77, G * D)), dev(f16(rng, 77, G * D)), 0)
+    c.set_pos(70)
+    c.set_len(7, 77)
+    d = Cache(cfg, capacity=16)
+    d.copy_from(c)
+    assert d.pos == 70 and d.len(3) == 70 and d.len(7) == 77 and d.capacity == c.capacity
+    bin_p, json_p = str(tmp_path / "c.bin"), str(tmp_path / "c.json")
+    c.save(bin_p, json_p)
+    e = Cache.load(bin_p, json_p, cfg)
+    assert e.pos == 70 and e.len(3) == 70 and e.len(7) == 77
+    for layer in c.full_layers:
+        a, b, x = c.download(layer, rows=c.capacity), d.download(layer, rows=c.capacity), \
+            e.download(layer, rows=c.capacity)
+        for i in range(2):
+            assert np.array_equal(a[i].view(np.uint16), b[i].view(np.uint16))
+            assert np.array_equal(a[i].view(np.uint16), x[i].view(np.uint16))
