@@ -46,6 +46,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="bounded CPU-baseline sample length")
     p.add_argument("--only", default="", help="comma list of decode,prefill,verify,ragged")
+    p.add_argument("--copy-calib", action="store_true",
+                   help="also run a plain 256 MiB device copy (reference for HBM counters)")
     return p.parse_args()
 
 
@@ -88,11 +90,13 @@ def main():
 
     def timed(fn, steps, warmup, backlog_ms):
         """Runs fn() warmup + steps times; the timed steps are queued behind
-        a GPU sleep of backlog_ms so events bracket device time only."""
+        a GPU sleep of backlog_ms so the two events bracket device time only.
+        A second pass of the same steps runs with the library's per-kernel
+        events on (read afterwards with _lib.prof_read); those events add
+        gaps between kernels, so they are kept out of the step timing."""
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
-        _lib.prof_enable(True)
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda._sleep(int(backlog_ms * cyc_per_ms))
         s.record()
@@ -100,10 +104,23 @@ def main():
             fn()
         e.record()
         torch.cuda.synchronize()
-        return s.elapsed_time(e) / steps  # ms per step
+        ms = s.elapsed_time(e) / steps  # ms per step
+        _lib.prof_enable(True)
+        torch.cuda._sleep(int(backlog_ms * cyc_per_ms))
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return ms
 
     print(f"[bench] start; sleep calib {cyc_per_ms:.0f} cycles/ms", file=sys.stderr, flush=True)
     rec = {}
+    if args.copy_calib:  # a kernel of known traffic: reads and writes 256 MiB once each
+        src = torch.empty(128 * 1024 * 1024, dtype=torch.float16, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     # ---------------------------------------------------------------- C2 decode
     if not only or "decode" in only:
@@ -194,10 +211,9 @@ def main():
         rng = np.random.default_rng(3)
         lengths = rng.integers(1024, 32769, size=64).astype(np.int32)
         offsets = np.zeros(64, np.int32)
-        offsets[1:] = np.cumsum((lengths + 7) // 8 * 8)[:-1]
-        rows = int(offsets[-1] + (lengths[-1] + 7) // 8 * 8)
-        k = randn(rows, G * D, seed=31)
-        vb = mi.kv_pack_v(randn(rows, G * D, seed=32), G)
+        offsets[1:] = np.cumsum((lengths + 31) // 32 * 32)[:-1]
+        rows = int(offsets[-1] + (lengths[-1] + 31) // 32 * 32)
+        k, vb = mi.kv_pack(randn(rows, G * D, seed=31), randn(rows, G * D, seed=32), G)
         q = randn(64, H, D, seed=33)
         g = randn(64, H, D, seed=34)
         out = torch.empty_like(q)
@@ -218,7 +234,7 @@ def main():
                          "split_kernel_us": split_us, "bytes": rbytes,
                          "sum_len": int(lengths.sum())}
         print(f"[bench] ragged {ms * 1000:.1f} us", file=sys.stderr, flush=True)
-        del k, vb
+        del k, vb  # k holds the packed K blocks
 
     # -------------------------------------------------------------- CPU baseline
     cpu = None

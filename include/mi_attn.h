@@ -18,14 +18,18 @@
  *     return MI_ERR_UNSUPPORTED.  Softmax scale is 1/sqrt(D), accumulation f32.
  *
  * Logical KV layout is the reference's token-major K[pos][kvh*D + i]
- * (src/math_util.rs:336).  Physical layout on the device (what
- * mi_kv_layer_ptrs and mi_attn_decode_ragged see):
- *   K: token-major, row r at  K + r*G*D            (unchanged from the reference)
+ * (src/math_util.rs:336); mi_kv_upload / mi_kv_download convert to and from
+ * token-major host rows, so callers that move cache contents through the
+ * host see the reference layout.  Physical layout on the device (what
+ * mi_kv_layer_ptrs, mi_kv_pack and mi_attn_decode_ragged see), chosen so
+ * that the MFMA operands of the decode kernel are whole 16-byte vectors and
+ * each 16-lane group of a wave reads 256 contiguous bytes:
+ *   K: 32-row blocks.  Row r = 32*b + w, element (r, h, i) at
+ *        K + (((b*G + h)*2 + u)*(D/8) + i/8)*128 + j*8 + i%8,
+ *      u = (w/4) % 2, j = 4*(w/8) + w%4.
  *   V: 8-row transposed blocks: element (r, h, i) at
- *        V + ((r/8)*G + h)*D*8 + i*8 + (r%8)
+ *        V + ((r/8)*G + h)*D*8 + i*8 + r%8
  *      so the eight keys of one value column are one 16-byte load.
- * mi_kv_upload / mi_kv_download convert to and from token-major host rows, so
- * callers that move cache contents through the host see the reference layout.
  */
 #ifndef MI_ATTN_H
 #define MI_ATTN_H
@@ -49,8 +53,9 @@ typedef enum mi_status {
   MI_ERR_UNSUPPORTED = 5    /* head shape the kernels are not built for     */
 } mi_status;
 
-/* Rows per V block of the device layout, and the granularity capacities are
- * rounded up to. */
+/* Rows per K block and per V block of the device layout, and the
+ * granularity capacities are rounded up to. */
+#define MI_KV_KBLOCK 32
 #define MI_KV_VBLOCK 8
 #define MI_KV_CAP_ALIGN 256
 
@@ -174,7 +179,7 @@ mi_status mi_attn_verify(mi_kv* kv, int32_t layer, const mi_f16* q,
 /* Ragged batched decode: `batch` independent sequences, one query token
  * each.  Sequence s owns rows [offsets[s], offsets[s] + lengths[s]) of the
  * shared k_rows / v_rows buffers (physical layout above with G KV heads;
- * offsets must be multiples of MI_KV_VBLOCK, the V buffer must hold whole
+ * offsets must be multiples of MI_KV_KBLOCK, the buffers must hold whole
  * blocks).  offsets, lengths: device int32[batch].  q, gate, out:
  * [batch][H][D].  max_len >= every lengths[s] bounds the launch grid.
  * No reference counterpart (the reference decodes one sequence,
@@ -192,12 +197,13 @@ mi_status mi_attn_decode_ragged(const mi_f16* k_rows, const mi_f16* v_rows,
                                 void* workspace, size_t workspace_bytes,
                                 mi_stream stream);
 
-/* Layout helpers for callers that build ragged buffers themselves: convert
- * `rows` token-major rows ([rows][G*D]) into the device V block layout
- * starting at block-aligned row `row0` of dst (device pointers, async). */
-mi_status mi_kv_pack_v(const mi_f16* src_rows, mi_f16* dst_v, int64_t row0,
-                       int64_t rows, int32_t num_kv_heads, int32_t head_dim,
-                       mi_stream stream);
+/* Layout helper for callers that build ragged buffers themselves: writes
+ * `rows` token-major rows k_rows, v_rows ([rows][G*D]) at rows
+ * [row0, row0+rows) of dst_k / dst_v in the device layout above (rows of
+ * partially covered blocks outside the range are kept).  Async. */
+mi_status mi_kv_pack(const mi_f16* k_rows, const mi_f16* v_rows, mi_f16* dst_k,
+                     mi_f16* dst_v, int64_t row0, int64_t rows,
+                     int32_t num_kv_heads, int32_t head_dim, mi_stream stream);
 
 /* ------------------------------------------------------------- profiling -- */
 

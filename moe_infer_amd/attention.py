@@ -24,6 +24,7 @@ import torch
 from . import _lib
 
 HEAD_DIM = 256
+KV_KBLOCK = 32
 KV_VBLOCK = 8
 
 
@@ -117,20 +118,24 @@ def attn_verify(cache, layer: int, q, k, v, past_pos: int, gate=None, out=None) 
     return out
 
 
-def kv_pack_v(rows: torch.Tensor, num_kv_heads: int, out: torch.Tensor | None = None,
-              row0: int = 0) -> torch.Tensor:
-    """Token-major V rows [n, G*D] -> the device 8-row block layout."""
+def kv_pack(k_rows: torch.Tensor, v_rows: torch.Tensor, num_kv_heads: int,
+            out: tuple[torch.Tensor, torch.Tensor] | None = None, row0: int = 0):
+    """Token-major K, V rows [n, G*D] -> (k_blocks, v_blocks) in the device
+    cache layout (32-row K blocks, 8-row transposed V blocks), written at rows
+    [row0, row0+n) of `out` (allocated zeroed, whole blocks, when None)."""
     G, D = num_kv_heads, HEAD_DIM
-    n = rows.numel() // (G * D)
+    n = k_rows.numel() // (G * D)
+    _check_tensor("k_rows", k_rows, n * G * D)
+    _check_tensor("v_rows", v_rows, n * G * D)
+    need = (row0 + n + KV_KBLOCK - 1) // KV_KBLOCK * KV_KBLOCK * G * D
     if out is None:
-        nblk = (row0 + n + KV_VBLOCK - 1) // KV_VBLOCK
-        out = torch.zeros(nblk * KV_VBLOCK * G * D, dtype=torch.float16, device=rows.device)
-    _check_tensor("rows", rows, n * G * D)
-    if out.numel() < ((row0 + n + KV_VBLOCK - 1) // KV_VBLOCK) * KV_VBLOCK * G * D:
-        raise ValueError("out too small for the packed blocks")
-    if row0 % KV_VBLOCK:
-        raise ValueError("row0 must be a multiple of 8")
-    _lib.check(_lib.lib().mi_kv_pack_v(_ptr(rows), _ptr(out), int(row0), n, G, D, _stream()))
+        out = (torch.zeros(need, dtype=torch.float16, device=k_rows.device),
+               torch.zeros(need, dtype=torch.float16, device=k_rows.device))
+    for t in out:
+        if t.numel() < need:
+            raise ValueError("output buffers hold fewer whole blocks than the rows need")
+    _lib.check(_lib.lib().mi_kv_pack(_ptr(k_rows), _ptr(v_rows), _ptr(out[0]), _ptr(out[1]),
+                                     int(row0), n, G, D, _stream()))
     return out
 
 
@@ -141,14 +146,14 @@ def ragged_workspace(batch: int, max_len: int, num_q_heads: int = 16, num_kv_hea
     return torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
-def attn_decode_ragged(k_rows: torch.Tensor, v_blocks: torch.Tensor, offsets: torch.Tensor,
+def attn_decode_ragged(k_blocks: torch.Tensor, v_blocks: torch.Tensor, offsets: torch.Tensor,
                        lengths: torch.Tensor, q: torch.Tensor, max_len: int,
                        num_kv_heads: int = 2, gate=None, out=None,
                        workspace: torch.Tensor | None = None,
                        validate: bool = True) -> torch.Tensor:
     """Ragged batch: sequence s uses rows [offsets[s], offsets[s]+lengths[s])
-    of k_rows (token-major [rows, G*D]) and v_blocks (8-row block layout,
-    see kv_pack_v).  q: [batch, H, D].  offsets must be multiples of 8."""
+    of k_blocks / v_blocks (the device cache layout, see kv_pack).
+    q: [batch, H, D].  offsets must be multiples of 32."""
     batch = offsets.numel()
     G, D = num_kv_heads, HEAD_DIM
     H = q.numel() // (batch * D)
@@ -160,21 +165,21 @@ def attn_decode_ragged(k_rows: torch.Tensor, v_blocks: torch.Tensor, offsets: to
     if out is None:
         out = torch.empty_like(q)
     _check_tensor("out", out, batch * H * D)
-    rows = k_rows.numel() // (G * D)
-    _check_tensor("k_rows", k_rows, rows * G * D)
-    nblk = (rows + KV_VBLOCK - 1) // KV_VBLOCK
-    if v_blocks.numel() < nblk * KV_VBLOCK * G * D:
-        raise ValueError("v_blocks holds fewer blocks than k_rows has rows")
+    rows = k_blocks.numel() // (G * D)
+    _check_tensor("k_blocks", k_blocks, rows * G * D)
+    if rows % KV_KBLOCK or v_blocks.numel() != k_blocks.numel():
+        raise ValueError("k_blocks / v_blocks must hold the same whole 32-row blocks")
+    _check_tensor("v_blocks", v_blocks, rows * G * D)
     if validate:  # host copy of the table (synchronises): bounds the kernel's reads
         off = offsets.cpu().tolist()
         ln = lengths.cpu().tolist()
         for s_, (o, n_) in enumerate(zip(off, ln)):
-            if o < 0 or o % KV_VBLOCK or n_ < 0 or n_ > max_len or o + n_ > rows:
+            if o < 0 or o % KV_KBLOCK or n_ < 0 or n_ > max_len or o + n_ > rows:
                 raise ValueError(f"sequence {s_}: offset {o}, length {n_} invalid for "
                                  f"{rows} rows, max_len {max_len}")
     if workspace is None:
         workspace = ragged_workspace(batch, max_len, H, G, q.device)
     _lib.check(_lib.lib().mi_attn_decode_ragged(
-        _ptr(k_rows), _ptr(v_blocks), _ptr(offsets), _ptr(lengths), batch, int(max_len), H, G,
+        _ptr(k_blocks), _ptr(v_blocks), _ptr(offsets), _ptr(lengths), batch, int(max_len), H, G,
         D, _ptr(q), _ptr(gate), _ptr(out), _ptr(workspace), workspace.numel(), _stream()))
     return out

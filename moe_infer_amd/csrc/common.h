@@ -30,6 +30,22 @@ void clear_error();
 // Checks the head shape the kernels are built for.
 mi_status check_shape(int32_t H, int32_t G, int32_t D);
 
+// Device layout of the cache (documented in mi_attn.h), in halves.
+// K: 32-row blocks; within a block, row w sits at A-operand row
+// j = 4*(w/8) + w%4 of half u = (w/4)%2, so that a 16-lane group reading
+// one 16-byte column chunk of 16 rows reads 256 contiguous bytes.
+__host__ __device__ inline int64_t k_offset(int64_t r, int h, int i, int G, int D) {
+  const int64_t b = r >> 5;
+  const int w = (int)(r & 31);
+  const int u = (w >> 2) & 1;
+  const int j = ((w >> 3) << 2) | (w & 3);
+  return (((b * G + h) * 2 + u) * (D / 8) + (i >> 3)) * 128 + j * 8 + (i & 7);
+}
+// V: 8-row transposed blocks, eight keys of one column contiguous.
+__host__ __device__ inline int64_t v_offset(int64_t r, int h, int i, int G, int D) {
+  return (((r >> 3) * G + h) * D + i) * 8 + (r & 7);
+}
+
 // Event pair around one launch when profiling is on (mi_prof_enable).
 void prof_begin(const char* name, hipStream_t s);
 void prof_end(const char* name, hipStream_t s);

@@ -37,7 +37,7 @@ constexpr int D = mi::kHeadDim;
 constexpr float kNegBig = -1e30f;
 
 struct SplitArgs {
-  const _Float16* k;        // K token-major, row r at k + r*G*D
+  const _Float16* k;        // K 32-row blocks (mi::k_offset)
   const _Float16* v;        // V blocks, (r,h,i) at v + ((r/8)*G + h)*D*8 + i*8 + r%8
   const int32_t* offsets;   // ragged: first row of sequence s (else null)
   const int32_t* lengths;   // ragged: rows of sequence s (else null)
@@ -57,18 +57,22 @@ __device__ __forceinline__ float xor_sum(float x, int mask) {
   return x + __shfl_xor(x, mask, 64);
 }
 
-// NW waves per workgroup; NCB column blocks of 16 columns
-// (column c = token (c / 8), query head in group (c % 8)).
-template <int NW, int NCB>
-__global__ void __launch_bounds__(NW * 64)
+// Workgroup = GH KV heads x NWH waves per head, over one chunk of keys of one
+// sequence (with GH = 2 a workgroup reads one contiguous stretch of both
+// heads' K and V blocks).  NCB column blocks of 16 columns (column c = token
+// c / 8, query head c % 8 of the group).
+template <int NWH, int NCB, int GH>
+__global__ void __launch_bounds__(NWH * GH * 64)
 attn_split_kernel(SplitArgs a) {
   extern __shared__ float smem[];
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  const int wv = threadIdx.x >> 6;
+  const int hw = wv / NWH;   // KV head of this wave within the workgroup
+  const int w = wv % NWH;    // wave within the head
   const int g = lane >> 4;   // lane group: k-slot group of the MFMA operands
   const int j = lane & 15;   // column within a column block / A-operand row
   const int chunk_idx = blockIdx.x;
-  const int kvh = blockIdx.y;
+  const int kvh = blockIdx.y * GH + hw;
   const int s = blockIdx.z;
   const int G = a.G;
   const int ncols = a.nq * 8;
@@ -79,7 +83,7 @@ attn_split_kernel(SplitArgs a) {
     row0 = a.offsets[s];
     lim0 = len;
     // invalid descriptors are reported as NaN by the combine kernel
-    if (len < 0 || len > a.kv_len || row0 < 0 || (row0 & 7)) return;
+    if (len < 0 || len > a.kv_len || row0 < 0 || (row0 & 31)) return;
   } else {
     len = a.kv_len;
     row0 = 0;
@@ -88,10 +92,10 @@ attn_split_kernel(SplitArgs a) {
   const int64_t key_begin = (int64_t)chunk_idx * a.chunk;
   if (key_begin >= len) return;  // uniform over the workgroup
   const int64_t key_end = min(key_begin + (int64_t)a.chunk, len);
-  const int64_t rstride = (int64_t)G * D;
 
-  // Q^T operand: lane (g, j) holds q[token][head][64g + 8kk + 0..7] for its
-  // column j, kk = 0..7.  Padding columns are zero and fully masked.
+  // Q^T operand: lane (g, j) holds q[token][head][32kk + 8g + 0..7] for its
+  // column j, kk = 0..7 (the column chunk 4kk + g the K operand of the same
+  // lane holds).  Padding columns are zero and fully masked.
   f16x8 qf[NCB][8];
   int64_t lim[NCB];
 #pragma unroll
@@ -100,9 +104,9 @@ attn_split_kernel(SplitArgs a) {
     const int tok = c >> 3;
     if (c < ncols) {
       const _Float16* qp =
-          a.q + (((int64_t)s * a.nq + tok) * a.H + kvh * 8 + (c & 7)) * D + 64 * g;
+          a.q + (((int64_t)s * a.nq + tok) * a.H + kvh * 8 + (c & 7)) * D + 8 * g;
 #pragma unroll
-      for (int kk = 0; kk < 8; kk++) qf[cb][kk] = *(const f16x8*)(qp + 8 * kk);
+      for (int kk = 0; kk < 8; kk++) qf[cb][kk] = *(const f16x8*)(qp + 32 * kk);
       lim[cb] = lim0 + tok;
     } else {
 #pragma unroll
@@ -121,18 +125,21 @@ attn_split_kernel(SplitArgs a) {
     for (int d = 0; d < 16; d++) acc[cb][d] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  const _Float16* kbase = a.k + row0 * rstride + kvh * D + 64 * g;
-  for (int64_t k0 = key_begin + 32 * w; k0 < key_end; k0 += 32 * NW) {
+  for (int64_t k0 = key_begin + 32 * w; k0 < key_end; k0 += 32 * NWH) {
     // K operand rows: tile u, A-row j <-> key k0 + 8*(j/4) + 4u + j%4, so that
-    // accumulator row 4g+e of tile u is key k0 + 8g + 4u + e.
+    // accumulator row 4g+e of tile u is key k0 + 8g + 4u + e.  In the 32-row
+    // block layout this operand (chunk 4kk + g of row j, half u) is one
+    // 16-byte vector, and the 16 lanes of a group read 256 contiguous bytes.
+    const _Float16* kp =
+        a.k + (((row0 + k0) >> 5) * G + kvh) * (int64_t)(32 * D) + g * 128 + j * 8;
     f16x8 kf[2][8];
 #pragma unroll
     for (int u = 0; u < 2; u++) {
       const int64_t key = k0 + 8 * (j >> 2) + 4 * u + (j & 3);
       if (key < key_end) {
-        const _Float16* kp = kbase + key * rstride;
 #pragma unroll
-        for (int kk = 0; kk < 8; kk++) kf[u][kk] = *(const f16x8*)(kp + 8 * kk);
+        for (int kk = 0; kk < 8; kk++)
+          kf[u][kk] = *(const f16x8*)(kp + u * (16 * D) + kk * 512);
       } else {
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) kf[u][kk] = f16x8{};
@@ -210,10 +217,12 @@ attn_split_kernel(SplitArgs a) {
     }
   }
 
-  // ---- merge the NW waves through LDS: [NW][ncols][D] O, [NW][ncols] m, l
-  float* so = smem;
-  float* sm = smem + NW * ncols * D;
-  float* sl = sm + NW * ncols;
+  // ---- merge the NWH waves of each head through LDS:
+  // per head [NWH][ncols][D] O, then [NWH][ncols] m and l
+  const int per_head = NWH * ncols * (D + 2);
+  float* so = smem + hw * per_head;
+  float* sm = so + NWH * ncols * D;
+  float* sl = sm + NWH * ncols;
 #pragma unroll
   for (int cb = 0; cb < NCB; cb++) {
     const int c = cb * 16 + j;
@@ -228,24 +237,29 @@ attn_split_kernel(SplitArgs a) {
     }
   }
   __syncthreads();
-  const int64_t pbase = (((int64_t)s * G + kvh) * a.max_chunks + chunk_idx) * ncols;
-  for (int idx = threadIdx.x; idx < ncols * D; idx += NW * 64) {
-    const int c = idx / D;
+  for (int idx = threadIdx.x; idx < GH * ncols * D; idx += NWH * GH * 64) {
+    const int h2 = idx / (ncols * D);
+    const int c = (idx / D) % ncols;
     const int d = idx % D;
+    const float* so2 = smem + h2 * per_head;
+    const float* sm2 = so2 + NWH * ncols * D;
+    const float* sl2 = sm2 + NWH * ncols;
     float M = kNegBig;
 #pragma unroll
-    for (int ww = 0; ww < NW; ww++) M = fmaxf(M, sm[ww * ncols + c]);
+    for (int ww = 0; ww < NWH; ww++) M = fmaxf(M, sm2[ww * ncols + c]);
     float o = 0.f, L = 0.f;
 #pragma unroll
-    for (int ww = 0; ww < NW; ww++) {
-      const float sc = exp2f(sm[ww * ncols + c] - M);
-      o += so[((int64_t)ww * ncols + c) * D + d] * sc;
-      L += sl[ww * ncols + c] * sc;
+    for (int ww = 0; ww < NWH; ww++) {
+      const float sc = exp2f(sm2[ww * ncols + c] - M);
+      o += so2[((int64_t)ww * ncols + c) * D + d] * sc;
+      L += sl2[ww * ncols + c] * sc;
     }
-    a.part_o[(pbase + c) * D + d] = o;
+    const int64_t pb =
+        (((int64_t)s * G + blockIdx.y * GH + h2) * a.max_chunks + chunk_idx) * ncols + c;
+    a.part_o[pb * D + d] = o;
     if (d == 0) {
-      a.part_ml[(pbase + c) * 2 + 0] = M;
-      a.part_ml[(pbase + c) * 2 + 1] = L;
+      a.part_ml[pb * 2 + 0] = M;
+      a.part_ml[pb * 2 + 1] = L;
     }
   }
 }
@@ -261,46 +275,112 @@ struct CombineArgs {
   int G, H, nq, chunk, max_chunks;
 };
 
-// One workgroup per (column, KV head, sequence); one thread per output
-// element of the head.  out = sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M),
-// zero when the denominator is zero (the reference's `sum > 0` guard and
-// zero-filled output, math_util.rs:357, 372), then * sigmoid(gate).
+// Chunk merge.  One workgroup per (column, KV head x 16-column slice,
+// sequence), 256 threads.  Two dependent global round trips: the partial
+// outputs o_c[d] are requested first (thread t: column d0 + t%16, chunks
+// congruent to t/16 mod 16, all loads independent), together with every
+// chunk's (m_c, l_c); the weights 2^(m_c - M) then come from one parallel
+// max-reduction in LDS.
+// out = sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M), zero when the
+// denominator is zero (the reference's `sum > 0` guard and zero-filled
+// output, math_util.rs:357, 372), then * sigmoid(gate).
+constexpr int kCombineSlice = 16;
+constexpr int kMaxChunks = 1024;
+
+__device__ __forceinline__ float block_reduce(float x, float* red, bool is_max) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float y = __shfl_xor(x, off, 64);
+    x = is_max ? fmaxf(x, y) : x + y;
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+  __syncthreads();
+  x = red[0];
+#pragma unroll
+  for (int i = 1; i < 4; i++) x = is_max ? fmaxf(x, red[i]) : x + red[i];
+  return x;
+}
+
 __global__ void __launch_bounds__(256)
 attn_combine_kernel(CombineArgs a) {
+  __shared__ float red[4];
+  __shared__ float wts[kMaxChunks];
+  __shared__ float acc_s[16][kCombineSlice + 1];
   const int c = blockIdx.x;
-  const int kvh = blockIdx.y;
+  const int kvh = blockIdx.y / (D / kCombineSlice);
+  const int d0 = (blockIdx.y % (D / kCombineSlice)) * kCombineSlice;
   const int s = blockIdx.z;
+  const int t = threadIdx.x;
   const int ncols = a.nq * 8;
   int64_t len = a.kv_len;
   bool bad = false;
   if (a.lengths) {
     len = a.lengths[s];
     const int32_t off = a.offsets[s];
-    bad = len < 0 || len > a.kv_len || off < 0 || (off & 7);
+    bad = len < 0 || len > a.kv_len || off < 0 || (off & 31);
     if (bad) len = 0;
   }
   const int nch = (int)((len + a.chunk - 1) / a.chunk);
   const int64_t pbase = ((int64_t)s * a.G + kvh) * a.max_chunks;
-  float M = kNegBig;
-  for (int ch = 0; ch < nch; ch++) M = fmaxf(M, a.part_ml[((pbase + ch) * ncols + c) * 2]);
-  const int tok = c >> 3;
-  const int hq = kvh * 8 + (c & 7);
-  const int64_t obase = (((int64_t)s * a.nq + tok) * a.H + hq) * D;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float o = 0.f, L = 0.f;
-    for (int ch = 0; ch < nch; ch++) {
-      const int64_t pi = (pbase + ch) * ncols + c;
-      const float sc = exp2f(a.part_ml[pi * 2] - M);
-      L += a.part_ml[pi * 2 + 1] * sc;
-      o += a.part_o[pi * D + d] * sc;
+  const float* ml = a.part_ml + (pbase * ncols + c) * 2;  // chunk ch at ml[ch * mstride]
+  const int64_t mstride = (int64_t)ncols * 2;
+  const int dl = t % kCombineSlice, cg = t / kCombineSlice;
+  const float* po = a.part_o + (pbase * ncols + c) * D + d0 + dl;
+  const int64_t ostride = (int64_t)ncols * D;
+
+  // first batch of partial outputs in flight before the statistics arrive
+  constexpr int kBatch = 8;
+  float ov[kBatch];
+#pragma unroll
+  for (int u = 0; u < kBatch; u++) {
+    const int ch = cg + 16 * u;
+    ov[u] = ch < nch ? po[ch * ostride] : 0.f;
+  }
+  float mloc[kMaxChunks / 256], lloc[kMaxChunks / 256];
+  float mx = kNegBig;
+#pragma unroll
+  for (int u = 0; u < kMaxChunks / 256; u++) {
+    const int ch = t + 256 * u;
+    mloc[u] = ch < nch ? ml[ch * mstride] : kNegBig;
+    lloc[u] = ch < nch ? ml[ch * mstride + 1] : 0.f;
+    mx = fmaxf(mx, mloc[u]);
+  }
+  const float M = block_reduce(mx, red, true);
+  float lsum = 0.f;
+#pragma unroll
+  for (int u = 0; u < kMaxChunks / 256; u++) {
+    const int ch = t + 256 * u;
+    if (ch < nch) {
+      const float wgt = exp2f(mloc[u] - M);
+      wts[ch] = wgt;
+      lsum += lloc[u] * wgt;
     }
-    float r = (L > 0.f) ? o / L : 0.f;
+  }
+  const float L = block_reduce(lsum, red, false);  // also publishes wts[]
+  float o = 0.f;
+#pragma unroll
+  for (int u = 0; u < kBatch; u++) {
+    const int ch = cg + 16 * u;
+    if (ch < nch) o += ov[u] * wts[ch];
+  }
+  for (int ch = cg + 16 * kBatch; ch < nch; ch += 16) o += po[ch * ostride] * wts[ch];
+  acc_s[cg][dl] = o;
+  __syncthreads();
+  if (t < kCombineSlice) {
+    float r = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) r += acc_s[i][t];
+    r = (L > 0.f) ? r / L : 0.f;
     if (bad) r = __builtin_nanf("");
+    const int tok = c >> 3;
+    const int hq = kvh * 8 + (c & 7);
+    const int64_t oidx = (((int64_t)s * a.nq + tok) * a.H + hq) * D + d0 + t;
     if (a.gate) {
-      const float gv = (float)a.gate[obase + d];
+      const float gv = (float)a.gate[oidx];
       r *= 1.f / (1.f + expf(-gv));
     }
-    a.out[obase + d] = (_Float16)r;
+    a.out[oidx] = (_Float16)r;
   }
 }
 
@@ -309,47 +389,57 @@ int env_int(const char* name, int dflt) {
   return (e && *e) ? atoi(e) : dflt;
 }
 
-// Keys per workgroup.  Target about two workgroups per CU (256 CUs) over the
-// whole launch, never less than one 32-key tile per wave.
-int pick_chunk(int nw, int64_t max_len, int64_t units) {
-  int forced = env_int("MI_ATTN_SPLIT_CHUNK", 0);
-  if (forced > 0) return (forced + 32 * nw - 1) / (32 * nw) * (32 * nw);
-  const int64_t step = 32 * nw;
-  int64_t target_wgs = 512;
-  int64_t chunks_per_unit = (target_wgs + units - 1) / units;
-  int64_t chunk = (max_len + chunks_per_unit - 1) / chunks_per_unit;
-  chunk = (chunk + step - 1) / step * step;
-  if (chunk < step) chunk = step;
-  return (int)chunk;
-}
-
 struct SplitPlan {
-  int nw, chunk, max_chunks;
+  int nwh, gh, ncb, chunk, max_chunks;
 };
 
-// Wave count and chunking of one split launch.  More than two query tokens
-// need 32 merge columns, which fit the 160 KB of LDS only with 4 waves.
-SplitPlan plan_split(int64_t max_len, int64_t units, int nq) {
+// Kernel variant and chunking of one split launch.  Keys per chunk (per
+// head): enough workgroups to cover 256 CUs about once (K/V of one key and
+// head is 1 KiB, so a 128-key chunk of two heads moves 256 KiB and leaves
+// one 8 KiB partial per head and query token), at least one 32-key tile per
+// wave, at most 2048 keys (ragged batches balance better with more
+// workgroups), and at most kMaxChunks chunks per sequence.
+SplitPlan plan_split(int64_t max_len, int64_t batch, int G, int nq) {
   SplitPlan p;
-  p.nw = (nq > 2 || env_int("MI_ATTN_SPLIT_WAVES", 8) == 4) ? 4 : 8;
-  p.chunk = pick_chunk(p.nw, max_len, units);
-  p.max_chunks = (int)((max_len + p.chunk - 1) / p.chunk);
+  p.ncb = nq <= 2 ? 1 : 2;
+  if (p.ncb == 2) {  // 32 columns: 4 waves, one head (registers and LDS)
+    p.nwh = 4;
+    p.gh = 1;
+  } else if (G % 2 == 0 && env_int("MI_ATTN_SPLIT_GH", 2) == 2) {
+    p.nwh = 4;
+    p.gh = 2;
+  } else {
+    p.nwh = 8;
+    p.gh = 1;
+  }
+  const int64_t step = 32 * p.nwh;
+  const int64_t target_wgs = env_int("MI_ATTN_SPLIT_WGS", 256);
+  int64_t chunk = env_int("MI_ATTN_SPLIT_CHUNK", 0);
+  if (chunk <= 0) {
+    chunk = (batch * G * max_len + p.gh * target_wgs - 1) / (p.gh * target_wgs);
+    if (chunk > 2048) chunk = 2048;
+  }
+  const int64_t min_chunk = (max_len + kMaxChunks - 1) / kMaxChunks;
+  if (chunk < min_chunk) chunk = min_chunk;
+  chunk = (chunk + step - 1) / step * step;
+  p.chunk = (int)chunk;
+  p.max_chunks = (int)((max_len + chunk - 1) / chunk);
   if (p.max_chunks < 1) p.max_chunks = 1;
   return p;
 }
 
-template <int NW, int NCB>
+template <int NWH, int NCB, int GH>
 mi_status launch_split(const SplitArgs& a, int64_t batch, hipStream_t stream) {
-  const size_t lds = ((size_t)NW * a.nq * 8 * (D + 2)) * sizeof(float);
+  const size_t lds = ((size_t)GH * NWH * a.nq * 8 * (D + 2)) * sizeof(float);
   static bool attr_done = false;
   if (!attr_done) {
-    MI_HIP(hipFuncSetAttribute((const void*)attn_split_kernel<NW, NCB>,
+    MI_HIP(hipFuncSetAttribute((const void*)attn_split_kernel<NWH, NCB, GH>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
     attr_done = true;
   }
-  dim3 grid(a.max_chunks, a.G, (unsigned)batch);
+  dim3 grid(a.max_chunks, a.G / GH, (unsigned)batch);
   mi::prof_begin("attn_split", stream);
-  attn_split_kernel<NW, NCB><<<grid, NW * 64, lds, stream>>>(a);
+  attn_split_kernel<NWH, NCB, GH><<<grid, NWH * GH * 64, lds, stream>>>(a);
   mi::prof_end("attn_split", stream);
   MI_HIP(hipGetLastError());
   return MI_OK;
@@ -366,8 +456,7 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
                     int64_t max_len, int64_t batch, int H, int G, int nq,
                     const _Float16* q, const _Float16* gate, _Float16* out,
                     void* ws, size_t ws_bytes, hipStream_t stream) {
-  const SplitPlan plan = plan_split(max_len, batch * G, nq);
-  const int nw = plan.nw;
+  const SplitPlan plan = plan_split(max_len, batch, G, nq);
   SplitArgs a;
   a.k = k;
   a.v = v;
@@ -388,11 +477,12 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
   a.part_o = (float*)ws;
   a.part_ml = a.part_o + (size_t)batch * G * a.max_chunks * nq * 8 * D;
   mi_status st;
-  if (nq <= 2) {
-    st = (nw == 8) ? launch_split<8, 1>(a, batch, stream) : launch_split<4, 1>(a, batch, stream);
-  } else {
-    st = launch_split<4, 2>(a, batch, stream);  // plan_split forces 4 waves here
-  }
+  if (plan.ncb == 2)
+    st = launch_split<4, 2, 1>(a, batch, stream);
+  else if (plan.gh == 2)
+    st = launch_split<4, 1, 2>(a, batch, stream);
+  else
+    st = launch_split<8, 1, 1>(a, batch, stream);
   MI_TRY(st);
   CombineArgs c;
   c.offsets = offsets;
@@ -407,7 +497,7 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
   c.nq = nq;
   c.chunk = a.chunk;
   c.max_chunks = a.max_chunks;
-  dim3 grid(nq * 8, G, (unsigned)batch);
+  dim3 grid(nq * 8, G * (D / kCombineSlice), (unsigned)batch);
   mi::prof_begin("attn_combine", stream);
   attn_combine_kernel<<<grid, 256, 0, stream>>>(c);
   mi::prof_end("attn_combine", stream);
@@ -430,7 +520,7 @@ mi_status cache_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float
   for (int32_t t0 = 0; t0 < n; t0 += 4) {
     const int nq = (n - t0) < 4 ? (n - t0) : 4;
     const int64_t rows = past_pos + t0 + nq;  // rows the last token of this group sees
-    const SplitPlan plan = plan_split(rows, kv->G, nq);
+    const SplitPlan plan = plan_split(rows, 1, kv->G, nq);
     void* ws;
     MI_TRY(mi::kv_workspace(kv, split_workspace_bytes(1, kv->G, plan.max_chunks, nq), &ws));
     const int64_t qoff = (int64_t)t0 * kv->H * D;
@@ -494,7 +584,7 @@ extern "C" size_t mi_attn_ragged_workspace_size(int32_t batch, int32_t max_len,
   if (batch <= 0 || max_len <= 0 || num_kv_heads <= 0) return 256;
   (void)num_q_heads;
   (void)head_dim;
-  const SplitPlan plan = plan_split(max_len, (int64_t)batch * num_kv_heads, 1);
+  const SplitPlan plan = plan_split(max_len, batch, num_kv_heads, 1);
   return split_workspace_bytes(batch, num_kv_heads, plan.max_chunks, 1);
 }
 

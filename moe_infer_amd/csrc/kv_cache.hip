@@ -9,10 +9,12 @@
 // kv_cache_append / kv_cache_append_n (src/engine/shaders.metal:2370-2383,
 // 2774-2792).
 //
-// Device layout (per layer): K token-major [cap][G*D]; V in 8-row transposed
-// blocks [cap/8][G][D][8], so one 16-byte load returns the eight keys of one
-// value column — the operand order the decode and prefill MFMA kernels
-// consume without an LDS transpose.
+// Device layout (per layer, mi::k_offset / mi::v_offset): K in 32-row blocks
+// whose 16-byte column chunks are ordered as the decode kernel's MFMA A
+// operand rows; V in 8-row transposed blocks [cap/8][G][D][8], so one
+// 16-byte load returns the eight keys of one value column — the operand
+// order the decode and prefill MFMA kernels consume without an LDS
+// transpose.
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -65,14 +67,20 @@ extern "C" void mi_roofline_peaks(double* hbm_gbps, double* f16_tflops) {
 
 // ------------------------------------------------------------- kernels ----
 
-// K rows: straight 16-byte copies of rows [pos, pos+n).
+// K rows into the 32-row block layout: one thread moves one 16-byte chunk
+// (8 consecutive columns of one head) of one row; chunks stay contiguous.
 __global__ void __launch_bounds__(256)
-kv_append_k_kernel(const f16x8* __restrict__ src, f16x8* __restrict__ dst,
-                   int64_t pos, int64_t n, int64_t vec_per_row) {
-  int64_t total = n * vec_per_row;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    dst[pos * vec_per_row + i] = src[i];
+kv_pack_k_kernel(const _Float16* __restrict__ src, _Float16* __restrict__ kblk,
+                 int64_t pos, int64_t n, int G, int D) {
+  const int cvec = D / 8;
+  const int64_t total = n * G * cvec;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t rr = idx / (G * cvec);
+    const int h = (int)((idx / cvec) % G);
+    const int c = (int)(idx % cvec);
+    *(f16x8*)(kblk + mi::k_offset(pos + rr, h, 8 * c, G, D)) =
+        *(const f16x8*)(src + rr * G * D + h * D + 8 * c);
   }
 }
 
@@ -198,23 +206,27 @@ mi_status kv_workspace(mi_kv* kv, size_t bytes, void** ws) {
   return MI_OK;
 }
 
+mi_status kv_pack_rows(const _Float16* k, const _Float16* v, _Float16* dst_k, _Float16* dst_v,
+                       int64_t pos, int64_t n, int G, int D, hipStream_t stream) {
+  const int64_t kthreads = n * G * (D / 8);
+  const int kgrid = (int)std::min<int64_t>((kthreads + 255) / 256, 4096);
+  kv_pack_k_kernel<<<kgrid, 256, 0, stream>>>(k, dst_k, pos, n, G, D);
+  MI_HIP(hipGetLastError());
+  const int64_t nblk = (pos + n - 1) / MI_KV_VBLOCK - pos / MI_KV_VBLOCK + 1;
+  const int64_t vthreads = nblk * G * (D / 8);
+  const int vgrid = (int)std::min<int64_t>((vthreads + 255) / 256, 4096);
+  kv_pack_v_kernel<<<vgrid, 256, 0, stream>>>(v, dst_v, pos, n, G, D);
+  MI_HIP(hipGetLastError());
+  return MI_OK;
+}
+
 mi_status kv_append_rows(mi_kv* kv, int32_t layer, const _Float16* k,
                          const _Float16* v, int64_t pos, int32_t n,
                          hipStream_t stream) {
-  const int64_t vec_per_row = (int64_t)kv->G * kv->D / 8;
-  int64_t kvec = (int64_t)n * vec_per_row;
-  int kgrid = (int)std::min<int64_t>((kvec + 255) / 256, 4096);
   mi::prof_begin("kv_append", stream);
-  kv_append_k_kernel<<<kgrid, 256, 0, stream>>>((const f16x8*)k, (f16x8*)kv->k[layer],
-                                                pos, n, vec_per_row);
-  MI_HIP(hipGetLastError());
-  int64_t nblk = (pos + n - 1) / MI_KV_VBLOCK - pos / MI_KV_VBLOCK + 1;
-  int64_t vthreads = nblk * kv->G * (kv->D / 8);
-  int vgrid = (int)std::min<int64_t>((vthreads + 255) / 256, 4096);
-  kv_pack_v_kernel<<<vgrid, 256, 0, stream>>>(v, kv->v[layer], pos, n, kv->G, kv->D);
+  mi_status st = kv_pack_rows(k, v, kv->k[layer], kv->v[layer], pos, n, kv->G, kv->D, stream);
   mi::prof_end("kv_append", stream);
-  MI_HIP(hipGetLastError());
-  return MI_OK;
+  return st;
 }
 
 }  // namespace mi
@@ -339,34 +351,48 @@ extern "C" mi_status mi_kv_append(mi_kv* kv, int32_t layer, const mi_f16* k,
   return MI_OK;
 }
 
-extern "C" mi_status mi_kv_pack_v(const mi_f16* src_rows, mi_f16* dst_v,
-                                  int64_t row0, int64_t rows,
-                                  int32_t num_kv_heads, int32_t head_dim,
-                                  mi_stream stream) {
+extern "C" mi_status mi_kv_pack(const mi_f16* k_rows, const mi_f16* v_rows, mi_f16* dst_k,
+                                mi_f16* dst_v, int64_t row0, int64_t rows,
+                                int32_t num_kv_heads, int32_t head_dim, mi_stream stream) {
   mi::clear_error();
-  if (!src_rows || !dst_v) return mi::fail(MI_ERR_INVALID_ARG, "null pointer");
+  if (!k_rows || !v_rows || !dst_k || !dst_v) return mi::fail(MI_ERR_INVALID_ARG, "null pointer");
   if (rows <= 0 || row0 < 0 || num_kv_heads <= 0 || head_dim <= 0 || head_dim % 8)
     return mi::fail(MI_ERR_INVALID_ARG, "bad pack arguments");
-  int64_t nblk = (row0 + rows - 1) / MI_KV_VBLOCK - row0 / MI_KV_VBLOCK + 1;
-  int64_t threads = nblk * num_kv_heads * (head_dim / 8);
-  int grid = (int)std::min<int64_t>((threads + 255) / 256, 4096);
-  kv_pack_v_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(
-      (const _Float16*)src_rows, (_Float16*)dst_v, row0, rows, num_kv_heads, head_dim);
-  MI_HIP(hipGetLastError());
-  return MI_OK;
+  return mi::kv_pack_rows((const _Float16*)k_rows, (const _Float16*)v_rows, (_Float16*)dst_k,
+                          (_Float16*)dst_v, row0, rows, num_kv_heads, head_dim,
+                          (hipStream_t)stream);
 }
 
 namespace {
 
-// Host copy of the V blocks covering rows [row0, row0+rows).
-mi_status download_v_blocks(const mi_kv* kv, int32_t layer, int64_t row0, int64_t rows,
-                            std::vector<_Float16>& blocks, int64_t* b0) {
-  *b0 = row0 / MI_KV_VBLOCK;
-  int64_t b1 = (row0 + rows - 1) / MI_KV_VBLOCK;
-  size_t per_block = (size_t)kv->G * kv->D * MI_KV_VBLOCK;
-  blocks.resize((size_t)(b1 - *b0 + 1) * per_block);
-  MI_HIP(hipMemcpy(blocks.data(), kv->v[layer] + *b0 * per_block,
-                   blocks.size() * sizeof(_Float16), hipMemcpyDeviceToHost));
+// Host image of the K and V blocks covering rows [row0, row0+rows) of one
+// layer, with accessors by (row, head, column).
+struct HostBlocks {
+  const mi_kv* kv;
+  int64_t kb0, vb0;  // first K / V block
+  std::vector<_Float16> k, v;
+  _Float16& K(int64_t r, int h, int i) {
+    return k[mi::k_offset(r, h, i, kv->G, kv->D) - kb0 * MI_KV_KBLOCK * kv->G * kv->D];
+  }
+  _Float16& V(int64_t r, int h, int i) {
+    return v[mi::v_offset(r, h, i, kv->G, kv->D) - vb0 * MI_KV_VBLOCK * kv->G * kv->D];
+  }
+};
+
+mi_status fetch_blocks(const mi_kv* kv, int32_t layer, int64_t row0, int64_t rows,
+                       HostBlocks& hb) {
+  const int64_t rl = (int64_t)kv->G * kv->D;
+  hb.kv = kv;
+  hb.kb0 = row0 / MI_KV_KBLOCK;
+  const int64_t kb1 = (row0 + rows - 1) / MI_KV_KBLOCK;
+  hb.vb0 = row0 / MI_KV_VBLOCK;
+  const int64_t vb1 = (row0 + rows - 1) / MI_KV_VBLOCK;
+  hb.k.resize((size_t)((kb1 - hb.kb0 + 1) * MI_KV_KBLOCK * rl));
+  hb.v.resize((size_t)((vb1 - hb.vb0 + 1) * MI_KV_VBLOCK * rl));
+  MI_HIP(hipMemcpy(hb.k.data(), kv->k[layer] + hb.kb0 * MI_KV_KBLOCK * rl,
+                   hb.k.size() * sizeof(_Float16), hipMemcpyDeviceToHost));
+  MI_HIP(hipMemcpy(hb.v.data(), kv->v[layer] + hb.vb0 * MI_KV_VBLOCK * rl,
+                   hb.v.size() * sizeof(_Float16), hipMemcpyDeviceToHost));
   return MI_OK;
 }
 
@@ -387,24 +413,21 @@ extern "C" mi_status mi_kv_upload(mi_kv* kv, int32_t layer, const mi_f16* host_k
   MI_TRY(check_rows(kv, row0, rows));
   if (rows == 0) return MI_OK;
   MI_HIP(hipDeviceSynchronize());
+  HostBlocks hb;
+  MI_TRY(fetch_blocks(kv, layer, row0, rows, hb));  // keeps rows outside the range
+  const _Float16* sk = (const _Float16*)host_k;
+  const _Float16* sv = (const _Float16*)host_v;
   const int64_t rl = (int64_t)kv->G * kv->D;
-  MI_HIP(hipMemcpy(kv->k[layer] + row0 * rl, host_k, (size_t)(rows * rl) * 2,
-                   hipMemcpyHostToDevice));
-  std::vector<_Float16> blocks;
-  int64_t b0;
-  MI_TRY(download_v_blocks(kv, layer, row0, rows, blocks, &b0));
-  const _Float16* src = (const _Float16*)host_v;
-  for (int64_t r = row0; r < row0 + rows; r++) {
-    int64_t b = r / MI_KV_VBLOCK - b0;
-    int rr = (int)(r % MI_KV_VBLOCK);
+  for (int64_t r = row0; r < row0 + rows; r++)
     for (int h = 0; h < kv->G; h++)
-      for (int i = 0; i < kv->D; i++)
-        blocks[((b * kv->G + h) * kv->D + i) * MI_KV_VBLOCK + rr] =
-            src[(r - row0) * rl + h * kv->D + i];
-  }
-  size_t per_block = (size_t)kv->G * kv->D * MI_KV_VBLOCK;
-  MI_HIP(hipMemcpy(kv->v[layer] + b0 * per_block, blocks.data(),
-                   blocks.size() * sizeof(_Float16), hipMemcpyHostToDevice));
+      for (int i = 0; i < kv->D; i++) {
+        hb.K(r, h, i) = sk[(r - row0) * rl + h * kv->D + i];
+        hb.V(r, h, i) = sv[(r - row0) * rl + h * kv->D + i];
+      }
+  MI_HIP(hipMemcpy(kv->k[layer] + hb.kb0 * MI_KV_KBLOCK * rl, hb.k.data(),
+                   hb.k.size() * sizeof(_Float16), hipMemcpyHostToDevice));
+  MI_HIP(hipMemcpy(kv->v[layer] + hb.vb0 * MI_KV_VBLOCK * rl, hb.v.data(),
+                   hb.v.size() * sizeof(_Float16), hipMemcpyHostToDevice));
   return MI_OK;
 }
 
@@ -416,21 +439,17 @@ extern "C" mi_status mi_kv_download(const mi_kv* kv, int32_t layer, mi_f16* host
   MI_TRY(check_rows(kv, row0, rows));
   if (rows == 0) return MI_OK;
   MI_HIP(hipDeviceSynchronize());
+  HostBlocks hb;
+  MI_TRY(fetch_blocks(kv, layer, row0, rows, hb));
+  _Float16* dk = (_Float16*)host_k;
+  _Float16* dv = (_Float16*)host_v;
   const int64_t rl = (int64_t)kv->G * kv->D;
-  MI_HIP(hipMemcpy(host_k, kv->k[layer] + row0 * rl, (size_t)(rows * rl) * 2,
-                   hipMemcpyDeviceToHost));
-  std::vector<_Float16> blocks;
-  int64_t b0;
-  MI_TRY(download_v_blocks(kv, layer, row0, rows, blocks, &b0));
-  _Float16* dst = (_Float16*)host_v;
-  for (int64_t r = row0; r < row0 + rows; r++) {
-    int64_t b = r / MI_KV_VBLOCK - b0;
-    int rr = (int)(r % MI_KV_VBLOCK);
+  for (int64_t r = row0; r < row0 + rows; r++)
     for (int h = 0; h < kv->G; h++)
-      for (int i = 0; i < kv->D; i++)
-        dst[(r - row0) * rl + h * kv->D + i] =
-            blocks[((b * kv->G + h) * kv->D + i) * MI_KV_VBLOCK + rr];
-  }
+      for (int i = 0; i < kv->D; i++) {
+        dk[(r - row0) * rl + h * kv->D + i] = hb.K(r, h, i);
+        dv[(r - row0) * rl + h * kv->D + i] = hb.V(r, h, i);
+      }
   return MI_OK;
 }
 

@@ -27,8 +27,12 @@ namespace {
 constexpr int D = mi::kHeadDim;
 constexpr int BQ = 128;        // queries per workgroup
 constexpr int BK = 64;         // keys per LDS tile
-constexpr int KROW = D + 8;    // padded K row in LDS (halves): 528 bytes
-constexpr int K_TILE_HALVES = BK * KROW;
+// K tile in LDS: two 32-key blocks copied verbatim from the cache layout
+// (mi::k_offset), each block's two row halves (u) separated by 128 bytes so
+// that the 16 lanes of an A-operand read hit distinct banks.
+constexpr int KU = 16 * D + 64;             // one u half + pad (halves)
+constexpr int KSUB = 2 * KU;                // one 32-key block
+constexpr int K_TILE_HALVES = 2 * KSUB;
 constexpr int V_TILE_HALVES = BK * D;  // 8 blocks of [D][8]
 constexpr int STAGE_HALVES = K_TILE_HALVES + V_TILE_HALVES;
 constexpr float kNegBig = -1e30f;
@@ -72,7 +76,6 @@ attn_prefill_kernel(PrefillArgs a) {
   const int qtile = a.ntiles - 1 - tile_rank;  // heaviest first
   const int hq = kvh * 8 + hg;
   const int q0 = qtile * BQ;
-  const int64_t G_D = (int64_t)a.G * D;
 
   // Q^T operand for this lane's query: 16 k-steps of 8 halves.
   const int qi = q0 + 32 * w + col;
@@ -105,8 +108,9 @@ attn_prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const int c = threadIdx.x + 256 * i;   // 0..2047
-      const int row = c >> 5, ch = c & 31;   // K: row, 16-byte chunk
-      kreg[i] = *(const f16x8*)(a.k + (key0 + row) * G_D + kvh * D + ch * 8);
+      // K: 16-byte chunk `c & 1023` of 32-key block `c >> 10` (contiguous)
+      kreg[i] = *(const f16x8*)(a.k + (((key0 >> 5) + (c >> 10)) * a.G + kvh) * (int64_t)(32 * D) +
+                                (c & 1023) * 8);
       const int blk = c >> 8, d = c & 255;   // V: block, column
       const int64_t gb = (key0 >> 3) + blk;
       f16x8 vv = *(const f16x8*)(a.v + ((gb * a.G + kvh) * D + d) * 8);
@@ -125,7 +129,7 @@ attn_prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const int c = threadIdx.x + 256 * i;
-      *(f16x8*)(ks + (c >> 5) * KROW + (c & 31) * 8) = kreg[i];
+      *(f16x8*)(ks + (c >> 10) * KSUB + ((c >> 9) & 1) * KU + (c & 511) * 8) = kreg[i];
       *(f16x8*)(vs + c * 8) = vreg[i];
     }
   };
@@ -144,11 +148,15 @@ attn_prefill_kernel(PrefillArgs a) {
       f32x16 st[2];
 #pragma unroll
       for (int sub = 0; sub < 2; sub++) {
-        const _Float16* kr = ks + (sub * 32 + qk_row_key(col)) * KROW + 8 * hl;
+        // A-operand row `col` is key qk_row_key(col) of the block; its chunk
+        // 2k + hl sits at (u, j) of the block layout.
+        const int key = qk_row_key(col);
+        const int u = (key >> 2) & 1, jr = ((key >> 3) << 2) | (key & 3);
+        const _Float16* kr = ks + sub * KSUB + u * KU + hl * 128 + jr * 8;
         f32x16 c16 = f32x16{};
 #pragma unroll
         for (int k = 0; k < 16; k++)
-          c16 = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8*)(kr + 16 * k), qf[k],
+          c16 = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8*)(kr + 256 * k), qf[k],
                                                        c16, 0, 0, 0);
         st[sub] = c16;
       }

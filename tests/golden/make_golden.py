@@ -40,8 +40,8 @@ def main():
         arrays.update({p + "q": q, p + "k": k, p + "v": v, p + "gate": g,
                        p + "out_f64": O.causal_f64(q, k, v, past, gate=g).astype(np.float32)})
     lengths = np.array([5, 0, 17], np.int32)
-    offsets = np.array([0, 8, 8], np.int32)
-    q, k, v = f16(rng, 3, H, D), f16(rng, 32, G * D), f16(rng, 32, G * D)
+    offsets = np.array([0, 32, 32], np.int32)
+    q, k, v = f16(rng, 3, H, D), f16(rng, 64, G * D), f16(rng, 64, G * D)
     arrays.update({"ragged_q": q, "ragged_k": k, "ragged_v": v, "ragged_offsets": offsets,
                    "ragged_lengths": lengths,
                    "ragged_out_f32": O.decode_ragged(q, k, v, offsets, lengths)})

@@ -48,7 +48,7 @@ def test_oracle_reproduces_ragged_fixture():
 def test_gpu_kernels_match_fixtures():
     import torch
 
-    from moe_infer_amd import Cache, attn_decode, attn_decode_ragged, attn_prefill, kv_pack_v
+    from moe_infer_amd import Cache, attn_decode, attn_decode_ragged, attn_prefill, kv_pack
 
     from .gpu_util import assert_close, dev
     for L in DECODE:
@@ -69,7 +69,8 @@ def test_gpu_kernels_match_fixtures():
                            gate=dev(c["gate"]))
         assert_close(out, c["out_f64"], f"fixture causal {name}")
     c = case("ragged_")
-    out = attn_decode_ragged(dev(c["k"]), kv_pack_v(dev(c["v"]), G),
+    kb, vb = kv_pack(dev(c["k"]), dev(c["v"]), G)
+    out = attn_decode_ragged(kb, vb,
                              torch.from_numpy(c["offsets"]).cuda(),
                              torch.from_numpy(c["lengths"]).cuda(), dev(c["q"]),
                              int(c["lengths"].max()))

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 import torch
 
-from moe_infer_amd import Cache, attn_decode, attn_decode_ragged, kv_cache_append, kv_pack_v
+from moe_infer_amd import Cache, attn_decode, attn_decode_ragged, kv_cache_append, kv_pack
 from oracle import oracle as O
 
 from .conftest import f16
@@ -20,8 +20,8 @@ def ragged_buffers(rng, lengths):
     offsets, rows = [], 0
     for n in lengths:
         offsets.append(rows)
-        rows += (n + 7) // 8 * 8  # sequences start on an 8-row block
-    rows = max(rows, 8)
+        rows += (n + 31) // 32 * 32  # sequences start on a 32-row block
+    rows = max(rows, 32)
     k, v = f16(rng, rows, G * D), f16(rng, rows, G * D)
     return np.array(offsets, np.int32), k, v
 
@@ -35,8 +35,8 @@ def test_ragged_matches_oracle(lengths):
     offsets, k, v = ragged_buffers(rng, lengths)
     b = len(lengths)
     q, g = f16(rng, b, H, D), f16(rng, b, H, D)
-    vb = kv_pack_v(dev(v), G)
-    out = attn_decode_ragged(dev(k), vb, torch.from_numpy(offsets).cuda(),
+    kb, vb = kv_pack(dev(k), dev(v), G)
+    out = attn_decode_ragged(kb, vb, torch.from_numpy(offsets).cuda(),
                              torch.from_numpy(lengths).cuda(), dev(q), int(lengths.max()),
                              gate=dev(g))
     ref = O.decode_ragged(q, k, v, offsets, lengths, gate=g)
@@ -54,7 +54,8 @@ def test_ragged_c3_shape():
     lengths = rng.integers(1024, 32769, size=64).astype(np.int32)
     offsets, k, v = ragged_buffers(rng, lengths)
     q = f16(rng, 64, H, D)
-    out = host(attn_decode_ragged(dev(k), kv_pack_v(dev(v), G), torch.from_numpy(offsets).cuda(),
+    kb, vb = kv_pack(dev(k), dev(v), G)
+    out = host(attn_decode_ragged(kb, vb, torch.from_numpy(offsets).cuda(),
                                   torch.from_numpy(lengths).cuda(), dev(q), 32768))
     for s in range(0, 64, 8):
         a, n = offsets[s], lengths[s]
@@ -71,22 +72,31 @@ def test_ragged_c3_shape():
 def test_ragged_rejects_bad_tables():
     rng = np.random.default_rng(0)
     k, v = f16(rng, 64, G * D), f16(rng, 64, G * D)
-    vb = kv_pack_v(dev(v), G)
+    kb, vb = kv_pack(dev(k), dev(v), G)
     q = dev(f16(rng, 2, H, D))
-    for off, ln in (([0, 3], [4, 4]), ([0, 8], [4, 100]), ([0, 8], [4, -1])):
+    for off, ln in (([0, 8], [4, 4]), ([0, 32], [4, 100]), ([0, 32], [4, -1]), ([0, 32], [4, 33])):
         with pytest.raises(ValueError):
-            attn_decode_ragged(dev(k), vb, torch.tensor(off, dtype=torch.int32).cuda(),
+            attn_decode_ragged(kb, vb, torch.tensor(off, dtype=torch.int32).cuda(),
                                torch.tensor(ln, dtype=torch.int32).cuda(), q, 64)
 
 
-def test_pack_v_layout():
-    """V rows land at ((r/8)*G + h)*D*8 + i*8 + r%8 (the documented layout)."""
+def test_pack_layout():
+    """Rows land where mi_attn.h documents: K at
+    (((b*G + h)*2 + u)*(D/8) + i/8)*128 + j*8 + i%8 with r = 32b + w,
+    u = (w/4)%2, j = 4*(w/8) + w%4; V at ((r/8)*G + h)*D*8 + i*8 + r%8."""
     rng = np.random.default_rng(11)
-    v = f16(rng, 21, G * D)
-    blk = host(kv_pack_v(dev(v), G)).reshape(-1, G, D, 8)
-    for r in range(21):
+    n = 45
+    k, v = f16(rng, n, G * D), f16(rng, n, G * D)
+    kb, vb = (host(t) for t in kv_pack(dev(k), dev(v), G))
+    kb = kb.reshape(-1, G, 2, D // 8, 16, 8)
+    vb = vb.reshape(-1, G, D, 8)
+    for r in range(n):
+        b, w = divmod(r, 32)
+        u, j = (w // 4) % 2, 4 * (w // 8) + w % 4
         for h in range(G):
-            assert np.array_equal(blk[r // 8, h, :, r % 8].view(np.uint16),
+            assert np.array_equal(kb[b, h, u, :, j, :].reshape(D).view(np.uint16),
+                                  k[r, h * D:(h + 1) * D].view(np.uint16))
+            assert np.array_equal(vb[r // 8, h, :, r % 8].view(np.uint16),
                                   v[r, h * D:(h + 1) * D].view(np.uint16))
 
 
