@@ -422,6 +422,7 @@ SplitPlan plan_split(int64_t max_len, int64_t batch, int G, int nq) {
   const int64_t min_chunk = (max_len + kMaxChunks - 1) / kMaxChunks;
   if (chunk < min_chunk) chunk = min_chunk;
   chunk = (chunk + step - 1) / step * step;
+  if (chunk < step) chunk = step;  // also for max_len == 0
   p.chunk = (int)chunk;
   p.max_chunks = (int)((max_len + chunk - 1) / chunk);
   if (p.max_chunks < 1) p.max_chunks = 1;
