@@ -168,7 +168,7 @@ def main():
         psteps = max(args.steps, 10)
         ms = timed(prefill_step, psteps, args.warmup, backlog_ms=30)
         pk_us, _ = _lib.prof_read("attn_prefill")
-        ap_us, _ = _lib.prof_read("kv_append")
+        ap_us = _lib.prof_read("kv_pack_k")[0] + _lib.prof_read("kv_pack_v")[0]
         _lib.prof_enable(False)
         rec["prefill"] = {
             "ms_per_step": ms, "kernel_us": pk_us, "append_us": ap_us,

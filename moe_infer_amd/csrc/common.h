@@ -3,6 +3,7 @@
 // layout of an mi_kv handle.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -46,9 +47,43 @@ __host__ __device__ inline int64_t v_offset(int64_t r, int h, int i, int G, int 
   return (((r >> 3) * G + h) * D + i) * 8 + (r & 7);
 }
 
-// Event pair around one launch when profiling is on (mi_prof_enable).
-void prof_begin(const char* name, hipStream_t s);
-void prof_end(const char* name, hipStream_t s);
+// Reductions across lanes that are 16 and 32 apart (the four 16-lane rows
+// of a wave), with the gfx950 row-swap instructions instead of LDS
+// permutes.  v_permlane16_swap exchanges rows 1 <-> 0 and 3 <-> 2 between
+// its two operands, v_permlane32_swap the upper and lower halves; with both
+// operands equal to x, the pair (r[0], r[1]) holds x of the two partners in
+// some order, so a symmetric op of the pair is the partner reduction.
+__device__ __forceinline__ float max_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_rows(float x) {  // max over lanes l, l^16, l^32, l^48
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return max_xor32(fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+}
+__device__ __forceinline__ float sum_rows(float x) {  // sum over lanes l, l^16, l^32, l^48
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return sum_xor32(__uint_as_float(r[0]) + __uint_as_float(r[1]));
+}
+
+// Timing event pair for one launch when profiling is on (mi_prof_enable),
+// else two nulls.
+void prof_events(const char* name, hipEvent_t* start, hipEvent_t* stop);
+
+// Launches a kernel of this library on `s`; with profiling on, the
+// dispatch's begin and end times are recorded under `name`.
+template <typename F, typename... Args>
+hipError_t launch(const char* name, F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                  Args... args) {
+  hipEvent_t a, b;
+  prof_events(name, &a, &b);
+  hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, s, a, b, 0u, args...);
+  return hipGetLastError();
+}
 
 }  // namespace mi
 

@@ -50,11 +50,14 @@ struct SplitArgs {
   float scale_log2e;
 };
 
-__device__ __forceinline__ float xor_max(float x, int mask) {
-  return fmaxf(x, __shfl_xor(x, mask, 64));
-}
-__device__ __forceinline__ float xor_sum(float x, int mask) {
-  return x + __shfl_xor(x, mask, 64);
+// 16-byte streaming load of K/V: read once per launch, so it is not kept in
+// the caches (MI_ATTN_TEMPORAL_KV=1 at build time keeps the default policy).
+__device__ __forceinline__ f16x8 load16(const _Float16* p) {
+#if defined(MI_ATTN_TEMPORAL_KV)
+  return *(const f16x8*)p;
+#else
+  return __builtin_nontemporal_load((const f16x8*)p);
+#endif
 }
 
 // Workgroup = GH KV heads x NWH waves per head, over one chunk of keys of one
@@ -132,39 +135,29 @@ attn_split_kernel(SplitArgs a) {
     // 16-byte vector, and the 16 lanes of a group read 256 contiguous bytes.
     const _Float16* kp =
         a.k + (((row0 + k0) >> 5) * G + kvh) * (int64_t)(32 * D) + g * 128 + j * 8;
+    // Whole 32-key tiles always lie inside the allocation (cache capacities
+    // are multiples of 256 rows; ragged sequences own whole 32-row blocks),
+    // so the loads are unconditional and straight-line.  Keys past key_end
+    // are masked out of the scores below; their V values are zeroed because
+    // stale rows may hold anything (NaN included) and 0 * NaN is NaN.
     f16x8 kf[2][8];
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-      const int64_t key = k0 + 8 * (j >> 2) + 4 * u + (j & 3);
-      if (key < key_end) {
+    for (int u = 0; u < 2; u++)
 #pragma unroll
-        for (int kk = 0; kk < 8; kk++)
-          kf[u][kk] = *(const f16x8*)(kp + u * (16 * D) + kk * 512);
-      } else {
-#pragma unroll
-        for (int kk = 0; kk < 8; kk++) kf[u][kk] = f16x8{};
-      }
-    }
+      for (int kk = 0; kk < 8; kk++) kf[u][kk] = load16(kp + u * (16 * D) + kk * 512);
     // V operand: lane (g, j), value block dblk holds V^T[dblk*16 + j][keys
     // k0+8g .. k0+8g+7] = one 16-byte vector of the block layout.
     f16x8 vf[16];
-    const int64_t vkey = k0 + 8 * g;
-    if (vkey < key_end) {
-      const _Float16* vp =
-          a.v + (((row0 + vkey) >> 3) * G + kvh) * (int64_t)(D * 8) + j * 8;
+    const _Float16* vp = a.v + (((row0 + k0) >> 3) + g) * G * (int64_t)(D * 8) + kvh * (D * 8) + j * 8;
 #pragma unroll
-      for (int dblk = 0; dblk < 16; dblk++) vf[dblk] = *(const f16x8*)(vp + dblk * 128);
-      if (vkey + 8 > key_end) {  // tail: rows past the end may be stale or NaN
-        const int valid = (int)(key_end - vkey);
+    for (int dblk = 0; dblk < 16; dblk++) vf[dblk] = load16(vp + dblk * 128);
+    if (k0 + 32 > key_end) {  // the last, partial tile (wave-uniform branch)
+      const int64_t valid = key_end - (k0 + 8 * g);
 #pragma unroll
-        for (int dblk = 0; dblk < 16; dblk++)
+      for (int dblk = 0; dblk < 16; dblk++)
 #pragma unroll
-          for (int e = 0; e < 8; e++)
-            if (e >= valid) vf[dblk][e] = (_Float16)0.f;
-      }
-    } else {
-#pragma unroll
-      for (int dblk = 0; dblk < 16; dblk++) vf[dblk] = f16x8{};
+        for (int e = 0; e < 8; e++)
+          if (e >= valid) vf[dblk][e] = (_Float16)0.f;
     }
 
 #pragma unroll
@@ -190,8 +183,7 @@ attn_split_kernel(SplitArgs a) {
           st[u][e] = x;
           mt = fmaxf(mt, x);
         }
-      mt = xor_max(mt, 16);
-      mt = xor_max(mt, 32);
+      mt = mi::max_rows(mt);
       const float mnew = fmaxf(m[cb], mt);
       const float alpha = exp2f(m[cb] - mnew);
       float rs = 0.f;
@@ -204,8 +196,7 @@ attn_split_kernel(SplitArgs a) {
           rs += p;
           pf[4 * u + e] = (_Float16)p;
         }
-      rs = xor_sum(rs, 16);
-      rs = xor_sum(rs, 32);
+      rs = mi::sum_rows(rs);
       l[cb] = l[cb] * alpha + rs;
       m[cb] = mnew;
 #pragma unroll
@@ -217,17 +208,20 @@ attn_split_kernel(SplitArgs a) {
     }
   }
 
-  // ---- merge the NWH waves of each head through LDS:
-  // per head [NWH][ncols][D] O, then [NWH][ncols] m and l
-  const int per_head = NWH * ncols * (D + 2);
+  // ---- merge the NWH waves of each head through LDS.  Per head:
+  // O [NWH][ncols][kLdsRow] (row padded by 4 floats so the 16 columns a
+  // lane group writes fall in distinct banks), then m, l [NWH][ncols], then
+  // the merge weights 2^(m_w - M) [NWH][ncols] and the merged l [ncols].
+  constexpr int kLdsRow = D + 4;
+  const int per_head = NWH * ncols * kLdsRow + 3 * NWH * ncols + ncols;
   float* so = smem + hw * per_head;
-  float* sm = so + NWH * ncols * D;
+  float* sm = so + NWH * ncols * kLdsRow;
   float* sl = sm + NWH * ncols;
 #pragma unroll
   for (int cb = 0; cb < NCB; cb++) {
     const int c = cb * 16 + j;
     if (c < ncols) {
-      float* dst = so + ((int64_t)w * ncols + c) * D + 4 * g;
+      float* dst = so + (w * ncols + c) * kLdsRow + 4 * g;
 #pragma unroll
       for (int dblk = 0; dblk < 16; dblk++) *(f32x4*)(dst + dblk * 16) = acc[cb][dblk];
       if (g == 0) {
@@ -237,30 +231,42 @@ attn_split_kernel(SplitArgs a) {
     }
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < GH * ncols * D; idx += NWH * GH * 64) {
-    const int h2 = idx / (ncols * D);
-    const int c = (idx / D) % ncols;
-    const int d = idx % D;
-    const float* so2 = smem + h2 * per_head;
-    const float* sm2 = so2 + NWH * ncols * D;
-    const float* sl2 = sm2 + NWH * ncols;
+  // weights: one thread per (head, column)
+  if ((int)threadIdx.x < GH * ncols) {
+    const int h2 = threadIdx.x / ncols, c = threadIdx.x % ncols;
+    float* sm2 = smem + h2 * per_head + NWH * ncols * kLdsRow;
+    float* sl2 = sm2 + NWH * ncols;
+    float* sw2 = sl2 + NWH * ncols;
     float M = kNegBig;
 #pragma unroll
     for (int ww = 0; ww < NWH; ww++) M = fmaxf(M, sm2[ww * ncols + c]);
-    float o = 0.f, L = 0.f;
+    float L = 0.f;
 #pragma unroll
     for (int ww = 0; ww < NWH; ww++) {
       const float sc = exp2f(sm2[ww * ncols + c] - M);
-      o += so2[((int64_t)ww * ncols + c) * D + d] * sc;
+      sw2[ww * ncols + c] = sc;
       L += sl2[ww * ncols + c] * sc;
     }
     const int64_t pb =
         (((int64_t)s * G + blockIdx.y * GH + h2) * a.max_chunks + chunk_idx) * ncols + c;
-    a.part_o[pb * D + d] = o;
-    if (d == 0) {
-      a.part_ml[pb * 2 + 0] = M;
-      a.part_ml[pb * 2 + 1] = L;
-    }
+    a.part_ml[pb * 2 + 0] = M;
+    a.part_ml[pb * 2 + 1] = L;
+  }
+  __syncthreads();
+  // merged O, four columns of d per thread
+  for (int idx = threadIdx.x; idx < GH * ncols * (D / 4); idx += NWH * GH * 64) {
+    const int h2 = idx / (ncols * (D / 4));
+    const int c = (idx / (D / 4)) % ncols;
+    const int d4 = (idx % (D / 4)) * 4;
+    const float* so2 = smem + h2 * per_head;
+    const float* sw2 = so2 + NWH * ncols * kLdsRow + 2 * NWH * ncols;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ww = 0; ww < NWH; ww++)
+      o += *(const f32x4*)(so2 + (ww * ncols + c) * kLdsRow + d4) * sw2[ww * ncols + c];
+    const int64_t pb =
+        (((int64_t)s * G + blockIdx.y * GH + h2) * a.max_chunks + chunk_idx) * ncols + c;
+    *(f32x4*)(a.part_o + pb * D + d4) = o;
   }
 }
 
@@ -276,35 +282,23 @@ struct CombineArgs {
 };
 
 // Chunk merge.  One workgroup per (column, KV head x 16-column slice,
-// sequence), 256 threads.  Two dependent global round trips: the partial
-// outputs o_c[d] are requested first (thread t: column d0 + t%16, chunks
-// congruent to t/16 mod 16, all loads independent), together with every
-// chunk's (m_c, l_c); the weights 2^(m_c - M) then come from one parallel
-// max-reduction in LDS.
+// sequence), 256 threads.  Every global load is issued up front: each
+// thread's (m_c, l_c) for chunks t, t+256, ... and its partial outputs o_c[d]
+// (column d0 + t%16, chunks congruent to t/16 mod 16, up to kBatch of
+// them).  The max and the sum over chunks are wave reductions in DPP
+// followed by one LDS exchange each.
 // out = sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M), zero when the
 // denominator is zero (the reference's `sum > 0` guard and zero-filled
 // output, math_util.rs:357, 372), then * sigmoid(gate).
 constexpr int kCombineSlice = 16;
 constexpr int kMaxChunks = 1024;
 
-__device__ __forceinline__ float block_reduce(float x, float* red, bool is_max) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float y = __shfl_xor(x, off, 64);
-    x = is_max ? fmaxf(x, y) : x + y;
-  }
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
-  __syncthreads();
-  x = red[0];
-#pragma unroll
-  for (int i = 1; i < 4; i++) x = is_max ? fmaxf(x, red[i]) : x + red[i];
-  return x;
-}
+extern "C" __device__ float __ockl_wfred_max_f32(float);
+extern "C" __device__ float __ockl_wfred_add_f32(float);
 
 __global__ void __launch_bounds__(256)
 attn_combine_kernel(CombineArgs a) {
-  __shared__ float red[4];
+  __shared__ float red[2][4];
   __shared__ float wts[kMaxChunks];
   __shared__ float acc_s[16][kCombineSlice + 1];
   const int c = blockIdx.x;
@@ -312,6 +306,7 @@ attn_combine_kernel(CombineArgs a) {
   const int d0 = (blockIdx.y % (D / kCombineSlice)) * kCombineSlice;
   const int s = blockIdx.z;
   const int t = threadIdx.x;
+  const int wv = t >> 6;
   const int ncols = a.nq * 8;
   int64_t len = a.kv_len;
   bool bad = false;
@@ -329,24 +324,27 @@ attn_combine_kernel(CombineArgs a) {
   const float* po = a.part_o + (pbase * ncols + c) * D + d0 + dl;
   const int64_t ostride = (int64_t)ncols * D;
 
-  // first batch of partial outputs in flight before the statistics arrive
-  constexpr int kBatch = 8;
+  float mloc[kMaxChunks / 256], lloc[kMaxChunks / 256];
+#pragma unroll
+  for (int u = 0; u < kMaxChunks / 256; u++) {
+    const int ch = t + 256 * u;
+    mloc[u] = ch < nch ? ml[ch * mstride] : kNegBig;
+    lloc[u] = ch < nch ? ml[ch * mstride + 1] : 0.f;
+  }
+  constexpr int kBatch = 16;
   float ov[kBatch];
 #pragma unroll
   for (int u = 0; u < kBatch; u++) {
     const int ch = cg + 16 * u;
     ov[u] = ch < nch ? po[ch * ostride] : 0.f;
   }
-  float mloc[kMaxChunks / 256], lloc[kMaxChunks / 256];
   float mx = kNegBig;
 #pragma unroll
-  for (int u = 0; u < kMaxChunks / 256; u++) {
-    const int ch = t + 256 * u;
-    mloc[u] = ch < nch ? ml[ch * mstride] : kNegBig;
-    lloc[u] = ch < nch ? ml[ch * mstride + 1] : 0.f;
-    mx = fmaxf(mx, mloc[u]);
-  }
-  const float M = block_reduce(mx, red, true);
+  for (int u = 0; u < kMaxChunks / 256; u++) mx = fmaxf(mx, mloc[u]);
+  mx = __ockl_wfred_max_f32(mx);
+  if ((t & 63) == 0) red[0][wv] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
   float lsum = 0.f;
 #pragma unroll
   for (int u = 0; u < kMaxChunks / 256; u++) {
@@ -357,7 +355,10 @@ attn_combine_kernel(CombineArgs a) {
       lsum += lloc[u] * wgt;
     }
   }
-  const float L = block_reduce(lsum, red, false);  // also publishes wts[]
+  lsum = __ockl_wfred_add_f32(lsum);
+  if ((t & 63) == 0) red[1][wv] = lsum;
+  __syncthreads();  // publishes wts[] and the wave sums
+  const float L = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
   float o = 0.f;
 #pragma unroll
   for (int u = 0; u < kBatch; u++) {
@@ -431,7 +432,9 @@ SplitPlan plan_split(int64_t max_len, int64_t batch, int G, int nq) {
 
 template <int NWH, int NCB, int GH>
 mi_status launch_split(const SplitArgs& a, int64_t batch, hipStream_t stream) {
-  const size_t lds = ((size_t)GH * NWH * a.nq * 8 * (D + 2)) * sizeof(float);
+  const int ncols = a.nq * 8;
+  const size_t lds =
+      (size_t)GH * (NWH * ncols * (D + 4) + 3 * NWH * ncols + ncols) * sizeof(float);
   static bool attr_done = false;
   if (!attr_done) {
     MI_HIP(hipFuncSetAttribute((const void*)attn_split_kernel<NWH, NCB, GH>,
@@ -439,10 +442,8 @@ mi_status launch_split(const SplitArgs& a, int64_t batch, hipStream_t stream) {
     attr_done = true;
   }
   dim3 grid(a.max_chunks, a.G / GH, (unsigned)batch);
-  mi::prof_begin("attn_split", stream);
-  attn_split_kernel<NWH, NCB, GH><<<grid, NWH * GH * 64, lds, stream>>>(a);
-  mi::prof_end("attn_split", stream);
-  MI_HIP(hipGetLastError());
+  MI_HIP(mi::launch("attn_split", attn_split_kernel<NWH, NCB, GH>, grid, dim3(NWH * GH * 64),
+                    lds, stream, a));
   return MI_OK;
 }
 
@@ -499,10 +500,7 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
   c.chunk = a.chunk;
   c.max_chunks = a.max_chunks;
   dim3 grid(nq * 8, G * (D / kCombineSlice), (unsigned)batch);
-  mi::prof_begin("attn_combine", stream);
-  attn_combine_kernel<<<grid, 256, 0, stream>>>(c);
-  mi::prof_end("attn_combine", stream);
-  MI_HIP(hipGetLastError());
+  MI_HIP(mi::launch("attn_combine", attn_combine_kernel, grid, dim3(256), 0, stream, c));
   return MI_OK;
 }
 

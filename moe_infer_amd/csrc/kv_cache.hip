@@ -210,23 +210,20 @@ mi_status kv_pack_rows(const _Float16* k, const _Float16* v, _Float16* dst_k, _F
                        int64_t pos, int64_t n, int G, int D, hipStream_t stream) {
   const int64_t kthreads = n * G * (D / 8);
   const int kgrid = (int)std::min<int64_t>((kthreads + 255) / 256, 4096);
-  kv_pack_k_kernel<<<kgrid, 256, 0, stream>>>(k, dst_k, pos, n, G, D);
-  MI_HIP(hipGetLastError());
+  MI_HIP(mi::launch("kv_pack_k", kv_pack_k_kernel, dim3(kgrid), dim3(256), 0, stream, k, dst_k,
+                    pos, n, G, D));
   const int64_t nblk = (pos + n - 1) / MI_KV_VBLOCK - pos / MI_KV_VBLOCK + 1;
   const int64_t vthreads = nblk * G * (D / 8);
   const int vgrid = (int)std::min<int64_t>((vthreads + 255) / 256, 4096);
-  kv_pack_v_kernel<<<vgrid, 256, 0, stream>>>(v, dst_v, pos, n, G, D);
-  MI_HIP(hipGetLastError());
+  MI_HIP(mi::launch("kv_pack_v", kv_pack_v_kernel, dim3(vgrid), dim3(256), 0, stream, v, dst_v,
+                    pos, n, G, D));
   return MI_OK;
 }
 
 mi_status kv_append_rows(mi_kv* kv, int32_t layer, const _Float16* k,
                          const _Float16* v, int64_t pos, int32_t n,
                          hipStream_t stream) {
-  mi::prof_begin("kv_append", stream);
-  mi_status st = kv_pack_rows(k, v, kv->k[layer], kv->v[layer], pos, n, kv->G, kv->D, stream);
-  mi::prof_end("kv_append", stream);
-  return st;
+  return kv_pack_rows(k, v, kv->k[layer], kv->v[layer], pos, n, kv->G, kv->D, stream);
 }
 
 }  // namespace mi

@@ -174,7 +174,7 @@ attn_prefill_kernel(PrefillArgs a) {
           st[sub][e] = x;
           mt = fmaxf(mt, x);
         }
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      mt = mi::max_xor32(mt);
       const float mnew = fmaxf(m, mt);
       const float alpha = exp2f(m - mnew);
       m = mnew;
@@ -188,7 +188,7 @@ attn_prefill_kernel(PrefillArgs a) {
           rs += p;
           pf[sub][e >> 3][e & 7] = (_Float16)p;
         }
-      rs += __shfl_xor(rs, 32, 64);
+      rs = mi::sum_xor32(rs);
       l = l * alpha + rs;
 #pragma unroll
       for (int i = 0; i < 8; i++) acc[i] *= alpha;
@@ -267,9 +267,6 @@ extern "C" mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
     attr_done = true;
   }
   const int grid = (a.work + 63) / 64 * 64;
-  mi::prof_begin("attn_prefill", s);
-  attn_prefill_kernel<<<grid, 256, lds, s>>>(a);
-  mi::prof_end("attn_prefill", s);
-  MI_HIP(hipGetLastError());
+  MI_HIP(mi::launch("attn_prefill", attn_prefill_kernel, dim3(grid), dim3(256), lds, s, a));
   return MI_OK;
 }

@@ -1,7 +1,8 @@
-// Per-kernel timing with HIP events recorded on the launch stream around
-// each kernel of the library (off by default).  bench.py reads the average
-// duration of the dominant kernel from here; rocprofv3 kernel traces of the
-// same run must agree with it.
+// Per-kernel timing (off by default): every kernel of the library is
+// launched with hipExtLaunchKernel, which stamps a start / stop event pair
+// with the dispatch's own begin and end times on the launch stream.  bench.py
+// reads the average duration of the dominant kernel from here; rocprofv3
+// kernel traces of the same run agree with it.
 #include <cstring>
 #include <map>
 #include <string>
@@ -13,7 +14,6 @@
 namespace {
 bool g_on = false;
 std::map<std::string, std::vector<std::pair<hipEvent_t, hipEvent_t>>> g_rec;
-std::map<std::string, hipEvent_t> g_open;
 
 void clear_all() {
   for (auto& kv : g_rec)
@@ -22,29 +22,22 @@ void clear_all() {
       (void)hipEventDestroy(p.second);
     }
   g_rec.clear();
-  for (auto& kv : g_open) (void)hipEventDestroy(kv.second);
-  g_open.clear();
 }
 }  // namespace
 
 namespace mi {
-void prof_begin(const char* name, hipStream_t s) {
+void prof_events(const char* name, hipEvent_t* start, hipEvent_t* stop) {
+  *start = *stop = nullptr;
   if (!g_on) return;
-  hipEvent_t e;
-  if (hipEventCreate(&e) != hipSuccess) return;
-  (void)hipEventRecord(e, s);
-  g_open[name] = e;
-}
-
-void prof_end(const char* name, hipStream_t s) {
-  if (!g_on) return;
-  auto it = g_open.find(name);
-  if (it == g_open.end()) return;
-  hipEvent_t e;
-  if (hipEventCreate(&e) != hipSuccess) return;
-  (void)hipEventRecord(e, s);
-  g_rec[name].emplace_back(it->second, e);
-  g_open.erase(it);
+  hipEvent_t a, b;
+  if (hipEventCreate(&a) != hipSuccess) return;
+  if (hipEventCreate(&b) != hipSuccess) {
+    (void)hipEventDestroy(a);
+    return;
+  }
+  g_rec[name].emplace_back(a, b);
+  *start = a;
+  *stop = b;
 }
 }  // namespace mi
 
