@@ -274,12 +274,25 @@ def main():
                                "256, f16 KV, sigmoid gate; step = 10 full-attention layers",
                    "batch": 1, "ctx": C2_CTX, "layers_per_step": LAYERS},
     }
+    # HBM bytes per launch measured by rocprofv3 counters (FETCH_SIZE + WRITE_SIZE,
+    # scaled by a plain copy of known size) for the same command; see
+    # profiles/attn_kernels_bench.md.  Null when the file is absent.
+    traffic = {}
+    tpath = ROOT / "profiles" / "traffic.json"
+    if tpath.exists():
+        traffic = json.loads(tpath.read_text())
+
+    def traffic_of(key):
+        e = traffic.get(key)
+        return None if e is None else e["read_bytes"] + e["write_bytes"]
+
     if d:
         line["decode_us_per_layer"] = round(d["us_per_layer"], 3)
         ach = C2_BYTES / (d["split_kernel_us"] * 1e3)
         line["roofline"] = {"bound": "hbm", "kernel": "attn_split_kernel (decode, C2)",
                             "achieved": round(ach, 1), "peak": hbm_peak, "unit": "GB/s",
-                            "frac": round(ach / hbm_peak, 4), "traffic": None}
+                            "frac": round(ach / hbm_peak, 4),
+                            "traffic": traffic_of("decode_split_c2")}
         line["decode"] = {k2: (round(v2, 3) if isinstance(v2, float) else v2)
                           for k2, v2 in d.items()}
     if p:
@@ -288,7 +301,7 @@ def main():
                                     "achieved": round(p["tflops_kernel"], 1), "peak": f16_peak,
                                     "unit": "TFLOP/s",
                                     "frac": round(p["tflops_kernel"] / f16_peak, 4),
-                                    "traffic": None}
+                                    "traffic": traffic_of("prefill_c4")}
         line["prefill"] = {k2: (round(v2, 3) if isinstance(v2, float) else v2)
                            for k2, v2 in p.items()}
     for key in ("verify", "ragged"):
