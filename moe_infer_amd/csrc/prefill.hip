@@ -88,71 +88,92 @@ attn_prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int ks = 0; ks < 16; ks++) qf[ks] = f16x8{};
   }
-  const int64_t qpos = a.past + qi;                     // this lane's query position
-  const int64_t wave_first = a.past + q0 + 32 * w;       // smallest query position of the wave
-  const int64_t wave_last = wave_first + 31;
-  const int64_t kv_len = a.past + a.n;
-  int64_t kv_end = a.past + q0 + BQ;
-  if (kv_end > kv_len) kv_end = kv_len;
-  const int nt = (int)((kv_end + BK - 1) / BK);
+  // In-kernel positions are 32-bit (the host checks past + n < 2^31).
+  const int past = (int)a.past;
+  const int qpos = past + qi;                  // this lane's query position
+  const int wave_first = past + q0 + 32 * w;   // smallest query position of the wave
+  const int wave_last = wave_first + 31;
+  const int kv_len = past + a.n;
+  const int kv_end = min(past + q0 + BQ, kv_len);
+  const int nt = (kv_end + BK - 1) / BK;
+  const float c2 = a.scale_log2e;
 
   f32x16 acc[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) acc[i] = f32x16{};
   float m = kNegBig, l = 0.f;
 
-  // Global -> register staging of one tile: 8 K chunks + 8 V chunks / thread.
-  f16x8 kreg[8], vreg[8];
-  auto load_tile = [&](int t) {
-    const int64_t key0 = (int64_t)t * BK;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const int c = threadIdx.x + 256 * i;   // 0..2047
-      // K: 16-byte chunk `c & 1023` of 32-key block `c >> 10` (contiguous)
-      kreg[i] = *(const f16x8*)(a.k + (((key0 >> 5) + (c >> 10)) * a.G + kvh) * (int64_t)(32 * D) +
-                                (c & 1023) * 8);
-      const int blk = c >> 8, d = c & 255;   // V: block, column
-      const int64_t gb = (key0 >> 3) + blk;
-      f16x8 vv = *(const f16x8*)(a.v + ((gb * a.G + kvh) * D + d) * 8);
-      const int64_t valid = kv_len - gb * 8;  // rows past the end may hold stale data
-      if (valid < 8) {
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-          if (e >= valid) vv[e] = (_Float16)0.f;
-      }
-      vreg[i] = vv;
-    }
-  };
-  auto store_tile = [&](int buf) {
+  // Tiles move global -> LDS directly (global_load_lds_dwordx4: each lane's
+  // 16 bytes land at the wave's LDS base + 16 * lane), no staging registers.
+  // A tile is 32 one-KiB pieces of K (two 32-key blocks of 16 KiB, each
+  // block's two row halves u placed KU apart) and 32 pieces of V (eight 4 KiB
+  // 8-key blocks, contiguous); wave w moves pieces 8w .. 8w+7 of each.
+  const int lane16 = lane * 8;  // halves
+  const _Float16* kg = a.k + (int64_t)kvh * (32 * D) + lane16;
+  const _Float16* vg = a.v + (int64_t)kvh * (D * 8) + lane16;
+  const int64_t kblk_stride = (int64_t)a.G * (32 * D);  // one 32-key block, all heads
+  const int64_t vblk_stride = (int64_t)a.G * (D * 8);   // one 8-key block, all heads
+  auto load_tile = [&](int t, int buf) {
+    const _Float16* kt = kg + (int64_t)(t * 2) * kblk_stride;
+    const _Float16* vt = vg + (int64_t)(t * 8) * vblk_stride;
     _Float16* ks = lds + buf * STAGE_HALVES;
     _Float16* vs = ks + K_TILE_HALVES;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const int c = threadIdx.x + 256 * i;
-      *(f16x8*)(ks + (c >> 10) * KSUB + ((c >> 9) & 1) * KU + (c & 511) * 8) = kreg[i];
-      *(f16x8*)(vs + c * 8) = vreg[i];
+    for (int pi = 0; pi < 8; pi++) {
+      const int i = 8 * w + pi;
+      const int b = i >> 4, u = (i >> 3) & 1, pc = i & 7;
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(kt + b * kblk_stride + (u * 8 + pc) * 512),
+          (__attribute__((address_space(3))) void*)(ks + b * KSUB + u * KU + pc * 512), 16, 0, 0);
+    }
+#pragma unroll
+    for (int pi = 0; pi < 8; pi++) {
+      const int i = 8 * w + pi;
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(vt + (i >> 2) * vblk_stride + (i & 3) * 512),
+          (__attribute__((address_space(3))) void*)(vs + i * 512), 16, 0, 0);
     }
   };
+  // Rows of the last tile past kv_len may hold stale data (NaN included):
+  // zero their V entries in LDS once the tile has landed.  Thread t owns
+  // value column t of every 8-key block.
+  auto zero_v_tail = [&](int t, int buf) {
+    _Float16* vs = lds + buf * STAGE_HALVES + K_TILE_HALVES;
+    for (int b = 0; b < 8; b++) {
+      const int valid = kv_len - (t * BK + 8 * b);
+      if (valid >= 8) continue;
+      _Float16* col8 = vs + (b * D + threadIdx.x) * 8;
+#pragma unroll
+      for (int e = 0; e < 8; e++)
+        if (e >= valid) col8[e] = (_Float16)0.f;
+    }
+  };
+  const bool tail_tile = (kv_len % BK) != 0;  // the last tile has rows past kv_len
 
-  load_tile(0);
-  store_tile(0);
+  // A-operand row `col` of each 32-key block is key qk_row_key(col); its
+  // chunk 2k + hl sits at (u, j) of the block layout.
+  const int krow = qk_row_key(col);
+  const int k_lds_off = ((krow >> 2) & 1) * KU + hl * 128 + (((krow >> 3) << 2) | (krow & 3)) * 8;
+
+  load_tile(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): this wave's pieces have landed
   __syncthreads();
+  if (tail_tile && nt == 1) {
+    zero_v_tail(0, 0);
+    __syncthreads();
+  }
 
   for (int t = 0; t < nt; t++) {
     const int buf = t & 1;
-    if (t + 1 < nt) load_tile(t + 1);
-    const int64_t key0 = (int64_t)t * BK;
+    if (t + 1 < nt) load_tile(t + 1, buf ^ 1);
+    const int key0 = t * BK;
     if (key0 <= wave_last) {
       const _Float16* ks = lds + buf * STAGE_HALVES;
       const _Float16* vs = ks + K_TILE_HALVES;
       f32x16 st[2];
 #pragma unroll
       for (int sub = 0; sub < 2; sub++) {
-        // A-operand row `col` is key qk_row_key(col) of the block; its chunk
-        // 2k + hl sits at (u, j) of the block layout.
-        const int key = qk_row_key(col);
-        const int u = (key >> 2) & 1, jr = ((key >> 3) << 2) | (key & 3);
-        const _Float16* kr = ks + sub * KSUB + u * KU + hl * 128 + jr * 8;
+        const _Float16* kr = ks + sub * KSUB + k_lds_off;
         f32x16 c16 = f32x16{};
 #pragma unroll
         for (int k = 0; k < 16; k++)
@@ -160,23 +181,24 @@ attn_prefill_kernel(PrefillArgs a) {
                                                        c16, 0, 0, 0);
         st[sub] = c16;
       }
-      const bool need_mask = key0 + BK - 1 > wave_first;
-      float mt = kNegBig;
+      // Raw scores; the scale (1/sqrt(D) * log2 e > 0) is folded into the
+      // exponent below, so the row max is taken on raw scores.
+      if (key0 + BK - 1 > wave_first) {  // diagonal tile: causal mask
+        const int rel = qpos - key0 - 8 * hl;  // key (key0 + 16 s2 + 8 hl + e7) <= qpos
+#pragma unroll
+        for (int sub = 0; sub < 2; sub++)
+#pragma unroll
+          for (int e = 0; e < 16; e++)
+            if (sub * 32 + 16 * (e >> 3) + (e & 7) > rel) st[sub][e] = -INFINITY;
+      }
+      float mt = st[0][0];
 #pragma unroll
       for (int sub = 0; sub < 2; sub++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-          float x = st[sub][e] * a.scale_log2e;
-          if (need_mask) {
-            const int64_t key = key0 + sub * 32 + 16 * (e >> 3) + 8 * hl + (e & 7);
-            x = (key <= qpos) ? x : -INFINITY;
-          }
-          st[sub][e] = x;
-          mt = fmaxf(mt, x);
-        }
-      mt = mi::max_xor32(mt);
+        for (int e = 0; e < 16; e++) mt = fmaxf(mt, st[sub][e]);
+      mt = mi::max_xor32(mt) * c2;
       const float mnew = fmaxf(m, mt);
-      const float alpha = exp2f(m - mnew);
+      const float alpha = __builtin_amdgcn_exp2f(m - mnew);
       m = mnew;
       float rs = 0.f;
       f16x8 pf[2][2];
@@ -184,14 +206,18 @@ attn_prefill_kernel(PrefillArgs a) {
       for (int sub = 0; sub < 2; sub++)
 #pragma unroll
         for (int e = 0; e < 16; e++) {
-          const float p = exp2f(st[sub][e] - mnew);
+          const float p = __builtin_amdgcn_exp2f(fmaf(st[sub][e], c2, -mnew));
           rs += p;
           pf[sub][e >> 3][e & 7] = (_Float16)p;
         }
       rs = mi::sum_xor32(rs);
       l = l * alpha + rs;
+      // Rescale only when some row max moved (wave-uniform branch); after the
+      // first tiles this is rare.
+      if (__ballot(alpha != 1.f)) {
 #pragma unroll
-      for (int i = 0; i < 8; i++) acc[i] *= alpha;
+        for (int i = 0; i < 8; i++) acc[i] *= alpha;
+      }
 #pragma unroll
       for (int sub = 0; sub < 2; sub++)
 #pragma unroll
@@ -204,8 +230,12 @@ attn_prefill_kernel(PrefillArgs a) {
                 *(const f16x8*)(vb + i * 32 * 8), pf[sub][stp], acc[i], 0, 0, 0);
         }
     }
-    if (t + 1 < nt) store_tile(buf ^ 1);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    if (tail_tile && t + 2 == nt) {
+      zero_v_tail(t + 1, buf ^ 1);
+      __syncthreads();
+    }
   }
 
   if (qi >= a.n) return;
@@ -242,6 +272,8 @@ extern "C" mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
   if (!q || !k || !v || !out) return mi::fail(MI_ERR_INVALID_ARG, "null q/k/v/out");
   if (n <= 0) return mi::fail(MI_ERR_INVALID_ARG, "n=%d", n);
   if (past_pos < 0) return mi::fail(MI_ERR_OUT_OF_RANGE, "past_pos=%lld", (long long)past_pos);
+  if (past_pos + n + 2 * BK >= ((int64_t)1 << 31))
+    return mi::fail(MI_ERR_OUT_OF_RANGE, "past_pos + n beyond 2^31 rows");
   // Tiles read up to 64 rows past the last key; capacity is a multiple of 256
   // rows, so it suffices that the rows themselves fit.
   MI_TRY(mi_kv_append(kv, layer, k, v, past_pos, n, stream));
