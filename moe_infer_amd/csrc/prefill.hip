@@ -34,7 +34,8 @@ constexpr int KU = 16 * D + 64;             // one u half + pad (halves)
 constexpr int KSUB = 2 * KU;                // one 32-key block
 constexpr int K_TILE_HALVES = 2 * KSUB;
 constexpr int V_TILE_HALVES = BK * D;  // 8 blocks of [D][8]
-constexpr int STAGE_HALVES = K_TILE_HALVES + V_TILE_HALVES;
+// LDS: K tiles double-buffered at [0, 2*K_TILE_HALVES), V tiles after them.
+constexpr int LDS_HALVES = 2 * (K_TILE_HALVES + V_TILE_HALVES);
 constexpr float kNegBig = -1e30f;
 
 struct PrefillArgs {
@@ -113,11 +114,11 @@ attn_prefill_kernel(PrefillArgs a) {
   const _Float16* vg = a.v + (int64_t)kvh * (D * 8) + lane16;
   const int64_t kblk_stride = (int64_t)a.G * (32 * D);  // one 32-key block, all heads
   const int64_t vblk_stride = (int64_t)a.G * (D * 8);   // one 8-key block, all heads
-  auto load_tile = [&](int t, int buf) {
+  _Float16* const kbuf0 = lds;
+  _Float16* const vbuf0 = lds + 2 * K_TILE_HALVES;
+  auto load_k = [&](int t) {
     const _Float16* kt = kg + (int64_t)(t * 2) * kblk_stride;
-    const _Float16* vt = vg + (int64_t)(t * 8) * vblk_stride;
-    _Float16* ks = lds + buf * STAGE_HALVES;
-    _Float16* vs = ks + K_TILE_HALVES;
+    _Float16* ks = kbuf0 + (t & 1) * K_TILE_HALVES;
 #pragma unroll
     for (int pi = 0; pi < 8; pi++) {
       const int i = 8 * w + pi;
@@ -126,6 +127,10 @@ attn_prefill_kernel(PrefillArgs a) {
           (const void*)(kt + b * kblk_stride + (u * 8 + pc) * 512),
           (__attribute__((address_space(3))) void*)(ks + b * KSUB + u * KU + pc * 512), 16, 0, 0);
     }
+  };
+  auto load_v = [&](int t) {
+    const _Float16* vt = vg + (int64_t)(t * 8) * vblk_stride;
+    _Float16* vs = vbuf0 + (t & 1) * V_TILE_HALVES;
 #pragma unroll
     for (int pi = 0; pi < 8; pi++) {
       const int i = 8 * w + pi;
@@ -137,8 +142,8 @@ attn_prefill_kernel(PrefillArgs a) {
   // Rows of the last tile past kv_len may hold stale data (NaN included):
   // zero their V entries in LDS once the tile has landed.  Thread t owns
   // value column t of every 8-key block.
-  auto zero_v_tail = [&](int t, int buf) {
-    _Float16* vs = lds + buf * STAGE_HALVES + K_TILE_HALVES;
+  auto zero_v_tail = [&](int t) {
+    _Float16* vs = vbuf0 + (t & 1) * V_TILE_HALVES;
     for (int b = 0; b < 8; b++) {
       const int valid = kv_len - (t * BK + 8 * b);
       if (valid >= 8) continue;
@@ -148,6 +153,7 @@ attn_prefill_kernel(PrefillArgs a) {
         if (e >= valid) col8[e] = (_Float16)0.f;
     }
   };
+
   const bool tail_tile = (kv_len % BK) != 0;  // the last tile has rows past kv_len
 
   // A-operand row `col` of each 32-key block is key qk_row_key(col); its
@@ -155,88 +161,127 @@ attn_prefill_kernel(PrefillArgs a) {
   const int krow = qk_row_key(col);
   const int k_lds_off = ((krow >> 2) & 1) * KU + hl * 128 + (((krow >> 3) << 2) | (krow & 3)) * 8;
 
-  load_tile(0, 0);
+  // P . V of one tile: O^T += V^T P^T over its 64 keys.
+  auto pv = [&](int t, const f16x8 (&pf)[2][2]) {
+    const _Float16* vs = vbuf0 + (t & 1) * V_TILE_HALVES;
+#pragma unroll
+    for (int sub = 0; sub < 2; sub++)
+#pragma unroll
+      for (int stp = 0; stp < 2; stp++) {
+        // V block of keys sub*32 + 16*stp + 8*hl .. +7
+        const _Float16* vb = vs + (sub * 4 + 2 * stp + hl) * (D * 8) + col * 8;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8*)(vb + i * 32 * 8),
+                                                          pf[sub][stp], acc[i], 0, 0, 0);
+      }
+  };
+
+  // Software pipeline over tiles: iteration t issues QK(t), then the PV
+  // MFMAs of tile t-1 (independent of QK(t)) run while the softmax of tile
+  // t executes on the VALU.  K runs one tile ahead of V: iteration t loads
+  // K(t+1) and V(t), so K and V each need only a double buffer.  After
+  // iteration t, acc = alpha_t * O_{t-1}; the epilogue adds P_{nt-1} V_{nt-1}.
+  load_k(0);
   __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): this wave's pieces have landed
   __syncthreads();
-  if (tail_tile && nt == 1) {
-    zero_v_tail(0, 0);
-    __syncthreads();
-  }
 
-  for (int t = 0; t < nt; t++) {
-    const int buf = t & 1;
-    if (t + 1 < nt) load_tile(t + 1, buf ^ 1);
-    const int key0 = t * BK;
-    if (key0 <= wave_last) {
-      const _Float16* ks = lds + buf * STAGE_HALVES;
-      const _Float16* vs = ks + K_TILE_HALVES;
-      f32x16 st[2];
+  f16x8 pprev[2][2];
+  bool pending = false;  // PV of the previous tile still to do
+  // QK^T of tile t: two 32-key sub-tiles, 16 k-steps each.
+  auto qk = [&](int t, f32x16 (&st)[2]) {
+    const _Float16* ks = kbuf0 + (t & 1) * K_TILE_HALVES;
 #pragma unroll
-      for (int sub = 0; sub < 2; sub++) {
-        const _Float16* kr = ks + sub * KSUB + k_lds_off;
-        f32x16 c16 = f32x16{};
+    for (int sub = 0; sub < 2; sub++) {
+      const _Float16* kr = ks + sub * KSUB + k_lds_off;
+      f32x16 c16 = f32x16{};
 #pragma unroll
-        for (int k = 0; k < 16; k++)
-          c16 = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8*)(kr + 256 * k), qf[k],
-                                                       c16, 0, 0, 0);
-        st[sub] = c16;
-      }
-      // Raw scores; the scale (1/sqrt(D) * log2 e > 0) is folded into the
-      // exponent below, so the row max is taken on raw scores.
-      if (key0 + BK - 1 > wave_first) {  // diagonal tile: causal mask
-        const int rel = qpos - key0 - 8 * hl;  // key (key0 + 16 s2 + 8 hl + e7) <= qpos
-#pragma unroll
-        for (int sub = 0; sub < 2; sub++)
-#pragma unroll
-          for (int e = 0; e < 16; e++)
-            if (sub * 32 + 16 * (e >> 3) + (e & 7) > rel) st[sub][e] = -INFINITY;
-      }
-      float mt = st[0][0];
-#pragma unroll
-      for (int sub = 0; sub < 2; sub++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) mt = fmaxf(mt, st[sub][e]);
-      mt = mi::max_xor32(mt) * c2;
-      const float mnew = fmaxf(m, mt);
-      const float alpha = __builtin_amdgcn_exp2f(m - mnew);
-      m = mnew;
-      float rs = 0.f;
-      f16x8 pf[2][2];
-#pragma unroll
-      for (int sub = 0; sub < 2; sub++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(st[sub][e], c2, -mnew));
-          rs += p;
-          pf[sub][e >> 3][e & 7] = (_Float16)p;
-        }
-      rs = mi::sum_xor32(rs);
-      l = l * alpha + rs;
-      // Rescale only when some row max moved (wave-uniform branch); after the
-      // first tiles this is rare.
-      if (__ballot(alpha != 1.f)) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) acc[i] *= alpha;
-      }
-#pragma unroll
-      for (int sub = 0; sub < 2; sub++)
-#pragma unroll
-        for (int stp = 0; stp < 2; stp++) {
-          // V block of keys sub*32 + 16*stp + 8*hl .. +7
-          const _Float16* vb = vs + (sub * 4 + 2 * stp + hl) * (D * 8) + col * 8;
-#pragma unroll
-          for (int i = 0; i < 8; i++)
-            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                *(const f16x8*)(vb + i * 32 * 8), pf[sub][stp], acc[i], 0, 0, 0);
-        }
+      for (int k = 0; k < 16; k++)
+        c16 = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8*)(kr + 256 * k), qf[k], c16,
+                                                     0, 0, 0);
+      st[sub] = c16;
     }
+  };
+  // Online softmax of one tile's raw scores: reference max, alpha, P (f16),
+  // l.  The scale (1/sqrt(D) * log2 e > 0) is folded into the exponent, so
+  // the row max is taken on raw scores.  The reference max m of a row moves
+  // only when the tile's max exceeds it by more than kLazy (base-2 units):
+  // P = 2^(s - m) then stays below 2^kLazy (well inside f16 and f32), the
+  // final normalisation divides by l accumulated against the same m, and
+  // the O rescale (alpha != 1) becomes rare.
+  constexpr float kLazy = 8.f;
+  auto softmax = [&](f32x16 (&st)[2], float& alpha) {
+    float mt = st[0][0];
+#pragma unroll
+    for (int sub = 0; sub < 2; sub++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) mt = fmaxf(mt, st[sub][e]);
+    mt = mi::max_xor32(mt) * c2;
+    const float mnew = (mt > m + kLazy) ? mt : m;
+    alpha = __builtin_amdgcn_exp2f(m - mnew);
+    m = mnew;
+    float rs = 0.f;
+#pragma unroll
+    for (int sub = 0; sub < 2; sub++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(st[sub][e], c2, -mnew));
+        rs += p;
+        pprev[sub][e >> 3][e & 7] = (_Float16)p;
+      }
+    rs = mi::sum_xor32(rs);
+    l = l * alpha + rs;
+  };
+  for (int t = 0; t < nt; t++) {
+    if (t + 1 < nt) load_k(t + 1);
+    load_v(t);
+    const int key0 = t * BK;
+    const bool active = key0 <= wave_last;
+    const bool diag = key0 + BK - 1 > wave_first;
+    float alpha = 1.f;
+    f32x16 st[2];
+    if (active && pending && !diag) {
+      // Steady state, one basic block: the PV MFMAs of tile t-1 are
+      // independent of tile t's softmax, so the scheduler can interleave the
+      // two (MFMA and VALU issue side by side).
+      qk(t, st);
+      f16x8 pcur[2][2];
+#pragma unroll
+      for (int a2 = 0; a2 < 2; a2++)
+#pragma unroll
+        for (int b2 = 0; b2 < 2; b2++) pcur[a2][b2] = pprev[a2][b2];
+      pv(t - 1, pcur);
+      softmax(st, alpha);
+    } else {
+      if (active) qk(t, st);
+      if (pending) pv(t - 1, pprev);
+      if (active) {
+        if (diag) {  // causal mask: key (key0 + 16 s2 + 8 hl + e7) <= qpos
+          const int rel = qpos - key0 - 8 * hl;
+#pragma unroll
+          for (int sub = 0; sub < 2; sub++)
+#pragma unroll
+            for (int e = 0; e < 16; e++)
+              if (sub * 32 + 16 * (e >> 3) + (e & 7) > rel) st[sub][e] = -INFINITY;
+        }
+        softmax(st, alpha);
+      }
+    }
+    // Rescale only when some row max moved (wave-uniform branch); after the
+    // first tiles this is rare.
+    if (__ballot(alpha != 1.f)) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) acc[i] *= alpha;
+    }
+    pending = active;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (tail_tile && t + 2 == nt) {
-      zero_v_tail(t + 1, buf ^ 1);
+    if (tail_tile && t + 1 == nt) {
+      zero_v_tail(t);
       __syncthreads();
     }
   }
+  if (pending) pv(nt - 1, pprev);
 
   if (qi >= a.n) return;
   const float inv = (l > 0.f) ? 1.f / l : 0.f;
@@ -292,7 +337,7 @@ extern "C" mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
   a.work = a.ntiles * kv->G * 8;
   a.scale_log2e = mi::kLog2e / sqrtf((float)D);
   static bool attr_done = false;
-  const size_t lds = 2 * STAGE_HALVES * sizeof(_Float16);
+  const size_t lds = LDS_HALVES * sizeof(_Float16);
   if (!attr_done) {
     MI_HIP(hipFuncSetAttribute((const void*)attn_prefill_kernel,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
