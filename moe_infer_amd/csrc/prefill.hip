@@ -116,6 +116,23 @@ attn_prefill_kernel(PrefillArgs a) {
   const int64_t vblk_stride = (int64_t)a.G * (D * 8);   // one 8-key block, all heads
   _Float16* const kbuf0 = lds;
   _Float16* const vbuf0 = lds + 2 * K_TILE_HALVES;
+  auto load_k_piece = [&](int t, int pi) {
+    const _Float16* kt = kg + (int64_t)(t * 2) * kblk_stride;
+    _Float16* ks = kbuf0 + (t & 1) * K_TILE_HALVES;
+    const int i = 8 * w + pi;
+    const int b = i >> 4, u = (i >> 3) & 1, pc = i & 7;
+    __builtin_amdgcn_global_load_lds(
+        (const void*)(kt + b * kblk_stride + (u * 8 + pc) * 512),
+        (__attribute__((address_space(3))) void*)(ks + b * KSUB + u * KU + pc * 512), 16, 0, 0);
+  };
+  auto load_v_piece = [&](int t, int pi) {
+    const _Float16* vt = vg + (int64_t)(t * 8) * vblk_stride;
+    _Float16* vs = vbuf0 + (t & 1) * V_TILE_HALVES;
+    const int i = 8 * w + pi;
+    __builtin_amdgcn_global_load_lds(
+        (const void*)(vt + (i >> 2) * vblk_stride + (i & 3) * 512),
+        (__attribute__((address_space(3))) void*)(vs + i * 512), 16, 0, 0);
+  };
   auto load_k = [&](int t) {
     const _Float16* kt = kg + (int64_t)(t * 2) * kblk_stride;
     _Float16* ks = kbuf0 + (t & 1) * K_TILE_HALVES;
@@ -188,19 +205,28 @@ attn_prefill_kernel(PrefillArgs a) {
 
   f16x8 pprev[2][2];
   bool pending = false;  // PV of the previous tile still to do
-  // QK^T of tile t: two 32-key sub-tiles, 16 k-steps each.
-  auto qk = [&](int t, f32x16 (&st)[2]) {
+  // QK^T of tile t: two 32-key sub-tiles, 16 k-steps each, the two chains
+  // interleaved.  With `dma`, the next tiles' global -> LDS pieces (K(t+1)
+  // piece i and V(t) piece i, i = 0..7) are issued between the MFMAs, so the
+  // issue stalls while the L2 -> LDS path drains overlap matrix work.
+  auto qk = [&](int t, f32x16 (&st)[2], bool dma) {
     const _Float16* ks = kbuf0 + (t & 1) * K_TILE_HALVES;
+    const _Float16* kr0 = ks + k_lds_off;
+    const _Float16* kr1 = ks + KSUB + k_lds_off;
+    f32x16 c0 = f32x16{}, c1 = f32x16{};
 #pragma unroll
-    for (int sub = 0; sub < 2; sub++) {
-      const _Float16* kr = ks + sub * KSUB + k_lds_off;
-      f32x16 c16 = f32x16{};
-#pragma unroll
-      for (int k = 0; k < 16; k++)
-        c16 = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8*)(kr + 256 * k), qf[k], c16,
-                                                     0, 0, 0);
-      st[sub] = c16;
+    for (int k = 0; k < 16; k++) {
+      c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8*)(kr0 + 256 * k), qf[k], c0, 0, 0,
+                                                  0);
+      c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8*)(kr1 + 256 * k), qf[k], c1, 0, 0,
+                                                  0);
+      if (dma) {
+        if ((k & 1) == 0) load_k_piece(t + 1, k >> 1);
+        else load_v_piece(t, k >> 1);
+      }
     }
+    st[0] = c0;
+    st[1] = c1;
   };
   // Online softmax of one tile's raw scores: reference max, alpha, P (f16),
   // l.  The scale (1/sqrt(D) * log2 e > 0) is folded into the exponent, so
@@ -233,18 +259,17 @@ attn_prefill_kernel(PrefillArgs a) {
     l = l * alpha + rs;
   };
   for (int t = 0; t < nt; t++) {
-    if (t + 1 < nt) load_k(t + 1);
-    load_v(t);
     const int key0 = t * BK;
     const bool active = key0 <= wave_last;
     const bool diag = key0 + BK - 1 > wave_first;
     float alpha = 1.f;
     f32x16 st[2];
     if (active && pending && !diag) {
-      // Steady state, one basic block: the PV MFMAs of tile t-1 are
-      // independent of tile t's softmax, so the scheduler can interleave the
-      // two (MFMA and VALU issue side by side).
-      qk(t, st);
+      // Steady state (a later tile holds this wave's diagonal, so t + 1 < nt),
+      // one basic block: QK(t) with the next tiles' DMA issue spread over its
+      // MFMAs, then PV(t-1), which is independent of tile t's softmax, so
+      // MFMA and VALU issue side by side.
+      qk(t, st, true);
       f16x8 pcur[2][2];
 #pragma unroll
       for (int a2 = 0; a2 < 2; a2++)
@@ -253,7 +278,9 @@ attn_prefill_kernel(PrefillArgs a) {
       pv(t - 1, pcur);
       softmax(st, alpha);
     } else {
-      if (active) qk(t, st);
+      if (t + 1 < nt) load_k(t + 1);
+      load_v(t);
+      if (active) qk(t, st, false);
       if (pending) pv(t - 1, pprev);
       if (active) {
         if (diag) {  // causal mask: key (key0 + 16 s2 + 8 hl + e7) <= qpos
