@@ -130,12 +130,21 @@ def main():
             v = randn(C2_CTX, G * D, seed=300 + layer)
             mi.kv_cache_append(cache, layer, k, v, 0)
             del k, v
-        cache.set_pos(C2_CTX)
         qs = [randn(H * D, seed=400 + i) for i in range(LAYERS)]
         gs = [randn(H * D, seed=500 + i) for i in range(LAYERS)]
+        kn = [randn(G * D, seed=600 + i) for i in range(LAYERS)]
+        vn = [randn(G * D, seed=700 + i) for i in range(LAYERS)]
         outs = [torch.empty(H * D, dtype=torch.float16, device=dev) for _ in range(LAYERS)]
+        pos = C2_CTX - 1  # the step's own token is row 32767: it attends 32768 rows
 
         def decode_step():
+            # the engine's per-layer attention step: append k, v at pos, attend
+            # rows [0, pos], sigmoid gate (one fused launch pair per layer)
+            for layer in range(LAYERS):
+                mi.attn_step(cache, layer, qs[layer], kn[layer], vn[layer], pos, gate=gs[layer],
+                             out=outs[layer])
+
+        def attend_only():
             for layer in range(LAYERS):
                 mi.attn_decode(cache, layer, qs[layer], C2_CTX, gate=gs[layer], out=outs[layer])
 
@@ -144,14 +153,19 @@ def main():
         split_us, n_split = _lib.prof_read("attn_split")
         comb_us, _ = _lib.prof_read("attn_combine")
         _lib.prof_enable(False)
+        ms_attend = timed(attend_only, args.steps, args.warmup,
+                          backlog_ms=args.steps * LAYERS * 0.25 + 20)
+        _lib.prof_enable(False)
         us_layer = ms * 1000 / LAYERS
         rec["decode"] = {
             "us_per_layer": us_layer, "gbps": C2_BYTES / (us_layer * 1e3),
+            "attend_only_us_per_layer": ms_attend * 1000 / LAYERS,
             "split_kernel_us": split_us, "combine_kernel_us": comb_us, "launches": n_split,
             "bytes_per_layer": C2_BYTES, "ms_per_step": ms,
         }
-        print(f"[bench] decode {us_layer:.2f} us/layer split {split_us:.2f} us", file=sys.stderr,
-              flush=True)
+        print(f"[bench] decode step {us_layer:.2f} us/layer (attend only "
+              f"{ms_attend * 100:.2f}) split {split_us:.2f} us combine {comb_us:.2f} us",
+              file=sys.stderr, flush=True)
         del cache
 
     # --------------------------------------------------------------- C4 prefill
@@ -168,7 +182,7 @@ def main():
         psteps = max(args.steps, 10)
         ms = timed(prefill_step, psteps, args.warmup, backlog_ms=30)
         pk_us, _ = _lib.prof_read("attn_prefill")
-        ap_us = _lib.prof_read("kv_pack_k")[0] + _lib.prof_read("kv_pack_v")[0]
+        ap_us = _lib.prof_read("kv_pack")[0]
         _lib.prof_enable(False)
         rec["prefill"] = {
             "ms_per_step": ms, "kernel_us": pk_us, "append_us": ap_us,
@@ -270,8 +284,9 @@ def main():
         "ms_per_step": round(d["ms_per_step"], 4) if d else None,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16", "data": "synthetic (seeded N(0,1) f16 q/K/V/gate)",
-        "config": {"workload": "C2: GQA decode, 1 token, ctx 32768, 16q/2kv heads, head_dim "
-                               "256, f16 KV, sigmoid gate; step = 10 full-attention layers",
+        "config": {"workload": "C2: GQA decode step (append the token's k/v, attend 32768 "
+                               "rows, sigmoid gate), 16q/2kv heads, head_dim 256, f16 KV; "
+                               "step = 10 full-attention layers",
                    "batch": 1, "ctx": C2_CTX, "layers_per_step": LAYERS},
     }
     # HBM bytes per launch measured by rocprofv3 counters (FETCH_SIZE + WRITE_SIZE,

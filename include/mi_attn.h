@@ -211,7 +211,7 @@ mi_status mi_kv_pack(const mi_f16* k_rows, const mi_f16* v_rows, mi_f16* dst_k,
  * stream (the reference's telemetry counterpart, src/engine.rs:13-24, at
  * kernel granularity).  mi_prof_enable synchronises the device and clears
  * earlier records.  Kernel names: "attn_split", "attn_combine",
- * "attn_prefill", "kv_pack_k", "kv_pack_v".
+ * "attn_prefill", "kv_pack".
  * mi_prof_read returns the mean duration in microseconds and the number of
  * launches recorded since the last enable. */
 void mi_prof_enable(int on);

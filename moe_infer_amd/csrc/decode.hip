@@ -48,6 +48,15 @@ struct SplitArgs {
   float* part_ml;           // [batch][G][max_chunks][ncols][2]
   int G, H, nq, chunk, max_chunks;
   float scale_log2e;
+  // Optional fused append (decode step, verify): rows [app0, app0 + app_n)
+  // of the cache are written from app_k / app_v ([app_n][G*D] token-major)
+  // by the workgroup whose key chunk holds them, before it reads them.
+  const _Float16* app_k;
+  const _Float16* app_v;
+  _Float16* kw;
+  _Float16* vw;
+  int64_t app0;
+  int app_n;
 };
 
 // 16-byte streaming load of K/V: read once per launch, so it is not kept in
@@ -95,6 +104,29 @@ attn_split_kernel(SplitArgs a) {
   const int64_t key_begin = (int64_t)chunk_idx * a.chunk;
   if (key_begin >= len) return;  // uniform over the workgroup
   const int64_t key_end = min(key_begin + (int64_t)a.chunk, len);
+
+  if (a.app_n > 0) {
+    // Fused append of the new rows that fall in this chunk, for this
+    // workgroup's GH heads; nothing else reads them in this launch.
+    const int64_t r_lo = max(key_begin, a.app0);
+    const int64_t r_hi = min(key_end, a.app0 + a.app_n);
+    if (r_lo < r_hi) {  // workgroup-uniform
+      const int nrow = (int)(r_hi - r_lo);
+      const int h0 = blockIdx.y * GH;
+      for (int it = threadIdx.x; it < nrow * GH * (D / 8); it += NWH * GH * 64) {
+        const int rr = it / (GH * (D / 8)), hh = (it / (D / 8)) % GH, c = it % (D / 8);
+        const int64_t r = r_lo + rr;
+        *(f16x8*)(a.kw + mi::k_offset(r, h0 + hh, 8 * c, G, D)) =
+            *(const f16x8*)(a.app_k + (r - a.app0) * G * D + (h0 + hh) * D + 8 * c);
+      }
+      for (int it = threadIdx.x; it < nrow * GH * D; it += NWH * GH * 64) {
+        const int rr = it / (GH * D), hh = (it / D) % GH, i = it % D;
+        const int64_t r = r_lo + rr;
+        a.vw[mi::v_offset(r, h0 + hh, i, G, D)] = a.app_v[(r - a.app0) * G * D + (h0 + hh) * D + i];
+      }
+      __syncthreads();  // the rows are in L2 before any wave of this group reads them
+    }
+  }
 
   // Q^T operand: lane (g, j) holds q[token][head][32kk + 8g + 0..7] for its
   // column j, kk = 0..7 (the column chunk 4kk + g the K operand of the same
@@ -249,8 +281,8 @@ attn_split_kernel(SplitArgs a) {
     }
     const int64_t pb =
         (((int64_t)s * G + blockIdx.y * GH + h2) * a.max_chunks + chunk_idx) * ncols + c;
-    a.part_ml[pb * 2 + 0] = M;
-    a.part_ml[pb * 2 + 1] = L;
+    __builtin_nontemporal_store(M, a.part_ml + pb * 2 + 0);
+    __builtin_nontemporal_store(L, a.part_ml + pb * 2 + 1);
   }
   __syncthreads();
   // merged O, four columns of d per thread
@@ -266,10 +298,12 @@ attn_split_kernel(SplitArgs a) {
       o += *(const f32x4*)(so2 + (ww * ncols + c) * kLdsRow + d4) * sw2[ww * ncols + c];
     const int64_t pb =
         (((int64_t)s * G + blockIdx.y * GH + h2) * a.max_chunks + chunk_idx) * ncols + c;
-    *(f32x4*)(a.part_o + pb * D + d4) = o;
+    __builtin_nontemporal_store(o, (f32x4*)(a.part_o + pb * D + d4));
   }
 }
 
+// Partials are written with streaming (non-temporal) stores: they are
+// consumed once, by the next kernel.
 struct CombineArgs {
   const int32_t* offsets;  // ragged (else null)
   const int32_t* lengths;  // ragged (else null)
@@ -453,11 +487,19 @@ size_t split_workspace_bytes(int64_t batch, int G, int max_chunks, int nq) {
 }
 
 // Runs split + combine for nq <= 4 query tokens per sequence.
+struct AppendRows {
+  const _Float16* k = nullptr;
+  const _Float16* v = nullptr;
+  int64_t row0 = 0;
+  int n = 0;
+};
+
 mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets,
                     const int32_t* lengths, int64_t kv_len, int64_t lim0,
                     int64_t max_len, int64_t batch, int H, int G, int nq,
                     const _Float16* q, const _Float16* gate, _Float16* out,
-                    void* ws, size_t ws_bytes, hipStream_t stream) {
+                    void* ws, size_t ws_bytes, hipStream_t stream,
+                    const AppendRows& app = AppendRows()) {
   const SplitPlan plan = plan_split(max_len, batch, G, nq);
   SplitArgs a;
   a.k = k;
@@ -473,6 +515,12 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
   a.chunk = plan.chunk;
   a.max_chunks = plan.max_chunks;
   a.scale_log2e = mi::kLog2e / sqrtf((float)D);
+  a.app_k = app.k;
+  a.app_v = app.v;
+  a.kw = const_cast<_Float16*>(k);
+  a.vw = const_cast<_Float16*>(v);
+  a.app0 = app.row0;
+  a.app_n = app.n;
   const size_t need = split_workspace_bytes(batch, G, a.max_chunks, nq);
   if (ws_bytes < need)
     return mi::fail(MI_ERR_INVALID_ARG, "workspace %zu bytes < %zu needed", ws_bytes, need);
@@ -513,8 +561,12 @@ mi_status check_layer(const mi_kv* kv, int32_t layer) {
 
 // Verify / decode over the cache: n query tokens at positions past_pos ..
 // past_pos+n-1, rows [0, past_pos+n) already in the cache.
+// With k_new / v_new, the n new rows [past_pos, past_pos + n) are appended
+// by the split kernels themselves (each token group appends its own rows,
+// which precede every read of them); the caller has grown the cache.
 mi_status cache_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float16* gate,
-                       _Float16* out, int64_t past_pos, int32_t n, hipStream_t stream) {
+                       _Float16* out, int64_t past_pos, int32_t n, hipStream_t stream,
+                       const _Float16* k_new = nullptr, const _Float16* v_new = nullptr) {
   const int64_t lim0 = past_pos + 1;
   for (int32_t t0 = 0; t0 < n; t0 += 4) {
     const int nq = (n - t0) < 4 ? (n - t0) : 4;
@@ -523,9 +575,16 @@ mi_status cache_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float
     void* ws;
     MI_TRY(mi::kv_workspace(kv, split_workspace_bytes(1, kv->G, plan.max_chunks, nq), &ws));
     const int64_t qoff = (int64_t)t0 * kv->H * D;
+    AppendRows app;
+    if (k_new) {
+      app.k = k_new + (int64_t)t0 * kv->G * D;
+      app.v = v_new + (int64_t)t0 * kv->G * D;
+      app.row0 = past_pos + t0;
+      app.n = nq;
+    }
     MI_TRY(run_split(kv->k[layer], kv->v[layer], nullptr, nullptr, rows, lim0 + t0,
                      rows, 1, kv->H, kv->G, nq, q + qoff, gate ? gate + qoff : nullptr,
-                     out + qoff, ws, kv->ws_bytes, stream));
+                     out + qoff, ws, kv->ws_bytes, stream, app));
   }
   return MI_OK;
 }
@@ -559,9 +618,12 @@ extern "C" mi_status mi_attn_step(mi_kv* kv, int32_t layer, const mi_f16* q,
   mi::clear_error();
   MI_TRY(check_layer(kv, layer));
   if (!q || !k || !v || !out) return mi::fail(MI_ERR_INVALID_ARG, "null q/k/v/out");
-  MI_TRY(mi_kv_append(kv, layer, k, v, pos, 1, stream));
-  return cache_attend(kv, layer, (const _Float16*)q, (const _Float16*)gate, (_Float16*)out,
-                      pos, 1, (hipStream_t)stream);
+  if (pos < 0) return mi::fail(MI_ERR_OUT_OF_RANGE, "pos=%lld", (long long)pos);
+  if (pos + 1 > kv->cap) MI_TRY(mi_kv_reserve(kv, pos + 1));
+  MI_TRY(cache_attend(kv, layer, (const _Float16*)q, (const _Float16*)gate, (_Float16*)out, pos,
+                      1, (hipStream_t)stream, (const _Float16*)k, (const _Float16*)v));
+  kv->len[layer] = pos + 1;
+  return MI_OK;
 }
 
 extern "C" mi_status mi_attn_verify(mi_kv* kv, int32_t layer, const mi_f16* q,
@@ -572,9 +634,12 @@ extern "C" mi_status mi_attn_verify(mi_kv* kv, int32_t layer, const mi_f16* q,
   MI_TRY(check_layer(kv, layer));
   if (!q || !k || !v || !out) return mi::fail(MI_ERR_INVALID_ARG, "null q/k/v/out");
   if (n <= 0) return mi::fail(MI_ERR_INVALID_ARG, "n=%d", n);
-  MI_TRY(mi_kv_append(kv, layer, k, v, past_pos, n, stream));
-  return cache_attend(kv, layer, (const _Float16*)q, (const _Float16*)gate, (_Float16*)out,
-                      past_pos, n, (hipStream_t)stream);
+  if (past_pos < 0) return mi::fail(MI_ERR_OUT_OF_RANGE, "past_pos=%lld", (long long)past_pos);
+  if (past_pos + n > kv->cap) MI_TRY(mi_kv_reserve(kv, past_pos + n));
+  MI_TRY(cache_attend(kv, layer, (const _Float16*)q, (const _Float16*)gate, (_Float16*)out,
+                      past_pos, n, (hipStream_t)stream, (const _Float16*)k, (const _Float16*)v));
+  kv->len[layer] = past_pos + n;
+  return MI_OK;
 }
 
 extern "C" size_t mi_attn_ragged_workspace_size(int32_t batch, int32_t max_len,

@@ -67,48 +67,45 @@ extern "C" void mi_roofline_peaks(double* hbm_gbps, double* f16_tflops) {
 
 // ------------------------------------------------------------- kernels ----
 
-// K rows into the 32-row block layout: one thread moves one 16-byte chunk
-// (8 consecutive columns of one head) of one row; chunks stay contiguous.
+// Writes n token-major rows k[n][G*D], v[n][G*D] at rows [pos, pos+n) of
+// the device layout, in one launch.  Work items [0, nk) are K chunks: one
+// 16-byte chunk (8 consecutive columns of one head) of one row, moved as is
+// (chunks stay contiguous in the 32-row block layout).  Items [nk, nk+nv)
+// are V columns: (8-row block b, head h, 8 consecutive columns d0..d0+7);
+// the thread gathers those columns of the block's rows that lie in
+// [pos, pos+n) and writes them as eight 16-byte column vectors (whole block
+// covered) or element by element (first/last partial block: rows outside
+// the range keep their contents).
 __global__ void __launch_bounds__(256)
-kv_pack_k_kernel(const _Float16* __restrict__ src, _Float16* __restrict__ kblk,
-                 int64_t pos, int64_t n, int G, int D) {
+kv_pack_kernel(const _Float16* __restrict__ k, const _Float16* __restrict__ v,
+               _Float16* __restrict__ kblk, _Float16* __restrict__ vblk, int64_t pos,
+               int64_t n, int G, int D) {
   const int cvec = D / 8;
-  const int64_t total = n * G * cvec;
-  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t rr = idx / (G * cvec);
-    const int h = (int)((idx / cvec) % G);
-    const int c = (int)(idx % cvec);
-    *(f16x8*)(kblk + mi::k_offset(pos + rr, h, 8 * c, G, D)) =
-        *(const f16x8*)(src + rr * G * D + h * D + 8 * c);
-  }
-}
-
-// V rows into the 8-row transposed block layout.  One thread owns
-// (block b, KV head h, 8 consecutive columns d0..d0+7): it gathers those
-// columns of the block's rows that lie in [pos, pos+n) and writes them
-// either as eight 16-byte column vectors (whole block covered) or element
-// by element (first/last partial block; rows outside the range keep their
-// contents).  src is token-major [n][G*D].
-__global__ void __launch_bounds__(256)
-kv_pack_v_kernel(const _Float16* __restrict__ src, _Float16* __restrict__ vblk,
-                 int64_t pos, int64_t n, int G, int D) {
+  const int64_t nk = n * G * cvec;
   const int64_t b_first = pos / MI_KV_VBLOCK;
   const int64_t b_last = (pos + n - 1) / MI_KV_VBLOCK;
-  const int cvec = D / 8;
-  const int64_t total = (b_last - b_first + 1) * G * cvec;
-  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+  const int64_t nv = (b_last - b_first + 1) * G * cvec;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < nk + nv;
        idx += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t b = b_first + idx / (G * cvec);
-    const int h = (int)((idx / cvec) % G);
-    const int d0 = (int)(idx % cvec) * 8;
+    if (idx < nk) {
+      const int64_t rr = idx / (G * cvec);
+      const int h = (int)((idx / cvec) % G);
+      const int c = (int)(idx % cvec);
+      *(f16x8*)(kblk + mi::k_offset(pos + rr, h, 8 * c, G, D)) =
+          *(const f16x8*)(k + rr * G * D + h * D + 8 * c);
+      continue;
+    }
+    const int64_t vi = idx - nk;
+    const int64_t b = b_first + vi / (G * cvec);
+    const int h = (int)((vi / cvec) % G);
+    const int d0 = (int)(vi % cvec) * 8;
     const int64_t r0 = b * MI_KV_VBLOCK;
     _Float16* blk = vblk + ((b * G + h) * (int64_t)D + d0) * MI_KV_VBLOCK;
     if (r0 >= pos && r0 + MI_KV_VBLOCK <= pos + n) {
       f16x8 rowv[8];
 #pragma unroll
       for (int rr = 0; rr < 8; rr++)
-        rowv[rr] = *(const f16x8*)(src + (r0 + rr - pos) * G * D + h * D + d0);
+        rowv[rr] = *(const f16x8*)(v + (r0 + rr - pos) * G * D + h * D + d0);
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         f16x8 col;
@@ -118,9 +115,9 @@ kv_pack_v_kernel(const _Float16* __restrict__ src, _Float16* __restrict__ vblk,
       }
     } else {
       for (int rr = 0; rr < 8; rr++) {
-        int64_t r = r0 + rr;
+        const int64_t r = r0 + rr;
         if (r < pos || r >= pos + n) continue;
-        f16x8 row = *(const f16x8*)(src + (r - pos) * G * D + h * D + d0);
+        const f16x8 row = *(const f16x8*)(v + (r - pos) * G * D + h * D + d0);
 #pragma unroll
         for (int i = 0; i < 8; i++) blk[i * MI_KV_VBLOCK + rr] = row[i];
       }
@@ -208,15 +205,11 @@ mi_status kv_workspace(mi_kv* kv, size_t bytes, void** ws) {
 
 mi_status kv_pack_rows(const _Float16* k, const _Float16* v, _Float16* dst_k, _Float16* dst_v,
                        int64_t pos, int64_t n, int G, int D, hipStream_t stream) {
-  const int64_t kthreads = n * G * (D / 8);
-  const int kgrid = (int)std::min<int64_t>((kthreads + 255) / 256, 4096);
-  MI_HIP(mi::launch("kv_pack_k", kv_pack_k_kernel, dim3(kgrid), dim3(256), 0, stream, k, dst_k,
-                    pos, n, G, D));
   const int64_t nblk = (pos + n - 1) / MI_KV_VBLOCK - pos / MI_KV_VBLOCK + 1;
-  const int64_t vthreads = nblk * G * (D / 8);
-  const int vgrid = (int)std::min<int64_t>((vthreads + 255) / 256, 4096);
-  MI_HIP(mi::launch("kv_pack_v", kv_pack_v_kernel, dim3(vgrid), dim3(256), 0, stream, v, dst_v,
-                    pos, n, G, D));
+  const int64_t items = (n + nblk) * G * (D / 8);
+  const int grid = (int)std::min<int64_t>((items + 255) / 256, 4096);
+  MI_HIP(mi::launch("kv_pack", kv_pack_kernel, dim3(grid), dim3(256), 0, stream, k, v, dst_k,
+                    dst_v, pos, n, G, D));
   return MI_OK;
 }
 
