@@ -205,13 +205,39 @@ mi_status mi_kv_pack(const mi_f16* k_rows, const mi_f16* v_rows, mi_f16* dst_k,
                      mi_f16* dst_v, int64_t row0, int64_t rows,
                      int32_t num_kv_heads, int32_t head_dim, mi_stream stream);
 
+/* ----------------------------------------------- Q/K head norm + RoPE -- */
+
+/* Largest rotary_dim mi_qk_norm_rope_append accepts. */
+#define MI_ROPE_MAX_DIM 256
+
+/* The step before attention, fused: per-head RMS norm of Q and K with bf16
+ * weights, NeoX partial rotary embedding of the first rotary_dim columns at
+ * position pos + t for token t, the Q/gate split of q_proj, and the append of
+ * the rotated K and the raw V rows at rows [pos, pos+n) of `layer`; then
+ * len(layer) = pos + n (grows the cache synchronously like mi_kv_append).
+ * Replaces q_head_norm_rope + k_head_norm_rope + kv_cache_append
+ * (src/math_util.rs:387-392, 501-593; src/engine/shaders.metal:2244-2383;
+ * called at src/engine/qwen35_moe/cpu.rs:126-145, fused_exp2.rs:630-680).
+ * q_proj: [n][H][2*D] f32, each head's query then gate; k, v: [n][G][D] f32;
+ * q_norm_w, k_norm_w: bf16 bit patterns [D]; q_out, gate_out: [n][H][D] f16.
+ * rotary_dim: multiple of 8, at most min(D, MI_ROPE_MAX_DIM) (the reference
+ * uses 64 = partial_rotary_factor * head_dim, rope_theta 1e7, eps 1e-6,
+ * qwen35_moe/constants.rs:166-167).  Async on `stream`. */
+mi_status mi_qk_norm_rope_append(mi_kv* kv, int32_t layer, const float* q_proj,
+                                 const float* k, const float* v,
+                                 const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                                 int32_t rotary_dim, float rope_theta, float eps,
+                                 int64_t pos, int32_t n, mi_f16* q_out,
+                                 mi_f16* gate_out, mi_stream stream);
+
 /* ------------------------------------------------------------- profiling -- */
 
 /* Kernel timing with HIP events stamped by each dispatch on its launch
  * stream (the reference's telemetry counterpart, src/engine.rs:13-24, at
  * kernel granularity).  mi_prof_enable synchronises the device and clears
  * earlier records.  Kernel names: "attn_split", "attn_combine",
- * "attn_prefill", "kv_pack".
+ * "attn_prefill", "kv_pack",
+ * "qk_norm_rope".
  * mi_prof_read returns the mean duration in microseconds and the number of
  * launches recorded since the last enable. */
 void mi_prof_enable(int on);

@@ -14,6 +14,8 @@ Reference operators these stand for (fbundle/moe_infer):
                 (src/engine/qwen35_moe/batched.rs:233-260)
   attn_verify   attn_sdpa_causal_n with past_pos = ctx and n = K drafts
   attn_decode_ragged  (no reference counterpart) independent sequences
+  qk_norm_rope_append  q_head_norm_rope + k_head_norm_rope + kv_cache_append
+                (src/math_util.rs:387-392, 501-593; shaders.metal:2244-2363)
 """
 from __future__ import annotations
 
@@ -75,6 +77,38 @@ def kv_cache_append(cache, layer: int, k: torch.Tensor, v: torch.Tensor, pos: in
     _check_kv_rows(cache, k, v, n)
     _lib.check(_lib.lib().mi_kv_append(cache._h, cache.slot(layer), _ptr(k), _ptr(v),
                                        int(pos), n, _stream()))
+
+
+def qk_norm_rope_append(cache, layer: int, q_proj: torch.Tensor, k: torch.Tensor,
+                        v: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor,
+                        pos: int, rotary_dim: int = 64, rope_theta: float = 1e7,
+                        eps: float = 1e-6, q_out=None, gate_out=None):
+    """Per-head RMS norm + NeoX partial RoPE of n tokens at positions
+    pos .. pos+n-1, fused with the cache append of the rotated K and raw V.
+
+    q_proj: [n, H, 2D] f32 (query then gate per head); k, v: [n, G, D] f32;
+    q_norm_w, k_norm_w: [D] bf16.  Returns (q, gate), each [n, H, D] f16.
+    len(layer) becomes pos + n."""
+    H, G, D = cache.num_q_heads, cache.num_kv_heads, cache.head_dim
+    n = q_proj.numel() // (H * 2 * D)
+    if n <= 0:
+        raise ValueError("q_proj holds no token")
+    _check_tensor("q_proj", q_proj, n * H * 2 * D, torch.float32)
+    _check_tensor("k", k, n * G * D, torch.float32)
+    _check_tensor("v", v, n * G * D, torch.float32)
+    _check_tensor("q_norm_w", q_norm_w, D, torch.bfloat16)
+    _check_tensor("k_norm_w", k_norm_w, D, torch.bfloat16)
+    if q_out is None:
+        q_out = torch.empty((n, H, D), dtype=torch.float16, device=q_proj.device)
+    if gate_out is None:
+        gate_out = torch.empty((n, H, D), dtype=torch.float16, device=q_proj.device)
+    _check_tensor("q_out", q_out, n * H * D)
+    _check_tensor("gate_out", gate_out, n * H * D)
+    _lib.check(_lib.lib().mi_qk_norm_rope_append(
+        cache._h, cache.slot(layer), _ptr(q_proj), _ptr(k), _ptr(v), _ptr(q_norm_w),
+        _ptr(k_norm_w), int(rotary_dim), float(rope_theta), float(eps), int(pos), n,
+        _ptr(q_out), _ptr(gate_out), _stream()))
+    return q_out, gate_out
 
 
 def attn_decode(cache, layer: int, q: torch.Tensor, seq_len: int,

@@ -349,3 +349,91 @@ ORACLE_API void oracle_attn_causal_n_f64(const uint16_t* q,
     oracle_attn_decode_f64(q + i * H * D, gate ? gate + i * H * D : NULL, k_rows,
                            v_rows, H, G, D, past_pos + i + 1, out + i * H * D);
 }
+
+/* ------------------------------------------------ Q/K head norm + RoPE -- */
+
+/* bf16 bit pattern -> f32 (exact). */
+ORACLE_API float oracle_bf16_to_f32(uint16_t b) {
+  uint32_t bits = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+/* RoPE inverse frequencies as the reference computes them in f32:
+ * rope_theta.powf(-2.0 * i / rotary_dim), i < rotary_dim / 2
+ * (src/math_util.rs:524, 531). */
+ORACLE_API void oracle_rope_inv_freq(float rope_theta, int64_t rotary_dim, float* out) {
+  for (int64_t i = 0; i < rotary_dim / 2; i++)
+    out[i] = powf(rope_theta, -2.0f * (float)i / (float)rotary_dim);
+}
+
+/* src/math_util.rs:501-547  q_head_norm_rope.  q_proj: [H][2*D] f32
+ * (query | gate per head); q_norm_w: bf16[D]; q_out, q_gate_out: [H][D]. */
+ORACLE_API void oracle_q_head_norm_rope(const float* q_proj, const uint16_t* q_norm_w,
+                                        float* q_out, float* q_gate_out, int64_t num_q_heads,
+                                        int64_t head_dim, int64_t rotary_dim, float rope_theta,
+                                        int64_t pos, float eps) {
+  int64_t rot_half = rotary_dim / 2;
+  for (int64_t h = 0; h < num_q_heads; h++) {
+    int64_t src_base = h * 2 * head_dim, out_base = h * head_dim;
+    for (int64_t d = 0; d < head_dim; d++) q_gate_out[out_base + d] = q_proj[src_base + head_dim + d];
+    float sum_sq = 0.0f;
+    for (int64_t d = 0; d < head_dim; d++) { float v = q_proj[src_base + d]; sum_sq += v * v; }
+    float inv_rms = 1.0f / sqrtf(sum_sq / (float)head_dim + eps);
+    for (int64_t d = 0; d < head_dim; d++) {
+      float q_val = q_proj[src_base + d] * inv_rms * oracle_bf16_to_f32(q_norm_w[d]);
+      if (d < rotary_dim) {
+        float cos_t, sin_t, pair_val;
+        if (d < rot_half) {
+          float theta = (float)pos * powf(rope_theta, -2.0f * (float)d / (float)rotary_dim);
+          pair_val = q_proj[src_base + d + rot_half] * inv_rms * oracle_bf16_to_f32(q_norm_w[d + rot_half]);
+          cos_t = cosf(theta); sin_t = sinf(theta);
+          q_out[out_base + d] = q_val * cos_t - pair_val * sin_t;
+        } else {
+          int64_t pair = d - rot_half;
+          float theta = (float)pos * powf(rope_theta, -2.0f * (float)pair / (float)rotary_dim);
+          pair_val = q_proj[src_base + pair] * inv_rms * oracle_bf16_to_f32(q_norm_w[pair]);
+          cos_t = cosf(theta); sin_t = sinf(theta);
+          q_out[out_base + d] = pair_val * sin_t + q_val * cos_t;
+        }
+      } else {
+        q_out[out_base + d] = q_val;
+      }
+    }
+  }
+}
+
+/* src/math_util.rs:553-593  k_head_norm_rope (in place on k_buf [G][D]). */
+ORACLE_API void oracle_k_head_norm_rope(float* k_buf, const uint16_t* k_norm_w,
+                                        int64_t num_kv_heads, int64_t head_dim,
+                                        int64_t rotary_dim, float rope_theta, int64_t pos,
+                                        float eps) {
+  int64_t rot_half = rotary_dim / 2;
+  float* orig = (float*)malloc(sizeof(float) * (size_t)head_dim);
+  for (int64_t h = 0; h < num_kv_heads; h++) {
+    int64_t base = h * head_dim;
+    float sum_sq = 0.0f;
+    for (int64_t d = 0; d < head_dim; d++) { float v = k_buf[base + d]; sum_sq += v * v; }
+    float inv_rms = 1.0f / sqrtf(sum_sq / (float)head_dim + eps);
+    for (int64_t d = 0; d < head_dim; d++) orig[d] = k_buf[base + d];
+    for (int64_t d = 0; d < head_dim; d++) {
+      float k_val = orig[d] * inv_rms * oracle_bf16_to_f32(k_norm_w[d]);
+      if (d < rotary_dim) {
+        if (d < rot_half) {
+          float theta = (float)pos * powf(rope_theta, -2.0f * (float)d / (float)rotary_dim);
+          float pair_val = orig[d + rot_half] * inv_rms * oracle_bf16_to_f32(k_norm_w[d + rot_half]);
+          k_buf[base + d] = k_val * cosf(theta) - pair_val * sinf(theta);
+        } else {
+          int64_t pair = d - rot_half;
+          float theta = (float)pos * powf(rope_theta, -2.0f * (float)pair / (float)rotary_dim);
+          float pair_val = orig[pair] * inv_rms * oracle_bf16_to_f32(k_norm_w[pair]);
+          k_buf[base + d] = pair_val * sinf(theta) + k_val * cosf(theta);
+        }
+      } else {
+        k_buf[base + d] = k_val;
+      }
+    }
+  }
+  free(orig);
+}

@@ -51,6 +51,11 @@ def lib() -> C.CDLL:
             "oracle_attn_decode_ragged_f16": (None, [P, P, P, P, P, P, I64, I64, I64, I64, P]),
             "oracle_attn_decode_f64": (None, [P, P, P, P, I64, I64, I64, I64, P]),
             "oracle_attn_causal_n_f64": (None, [P, P, P, P, I64, I64, I64, I64, I64, P]),
+            "oracle_bf16_to_f32": (C.c_float, [C.c_uint16]),
+            "oracle_rope_inv_freq": (None, [C.c_float, I64, P]),
+            "oracle_q_head_norm_rope": (None, [P, P, P, P, I64, I64, I64, C.c_float, I64,
+                                               C.c_float]),
+            "oracle_k_head_norm_rope": (None, [P, P, I64, I64, I64, C.c_float, I64, C.c_float]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -192,6 +197,34 @@ def decode_ragged(q, k_rows, v_rows, offsets, lengths, gate=None, H=16, G=2, D=2
     lib().oracle_attn_decode_ragged_f16(_p(q), _p(gate), _p(k_rows), _p(v_rows), _p(offsets),
                                         _p(lengths), b, H, G, D, _p(out))
     return out.reshape(b, H, D)
+
+
+# ------------------------------------------------ Q/K head norm + RoPE --
+
+def rope_inv_freq(rope_theta=1e7, rotary_dim=64):
+    out = np.empty(rotary_dim // 2, dtype=np.float32)
+    lib().oracle_rope_inv_freq(rope_theta, rotary_dim, _p(out))
+    return out
+
+
+def q_head_norm_rope(q_proj, q_norm_w, pos, H=16, D=256, rotary_dim=64, rope_theta=1e7,
+                     eps=1e-6):
+    """q_proj [H, 2D] (f32 values; f16 inputs are widened exactly), q_norm_w
+    bf16 bit patterns uint16[D] -> (q_out [H, D], gate [H, D]) f32."""
+    qp = _f(q_proj)
+    w = np.ascontiguousarray(q_norm_w, dtype=np.uint16)
+    q = np.empty(H * D, np.float32)
+    g = np.empty(H * D, np.float32)
+    lib().oracle_q_head_norm_rope(_p(qp), _p(w), _p(q), _p(g), H, D, rotary_dim, rope_theta,
+                                  pos, eps)
+    return q.reshape(H, D), g.reshape(H, D)
+
+
+def k_head_norm_rope(k, k_norm_w, pos, G=2, D=256, rotary_dim=64, rope_theta=1e7, eps=1e-6):
+    kb = np.array(k, dtype=np.float32, copy=True).reshape(-1)
+    w = np.ascontiguousarray(k_norm_w, dtype=np.uint16)
+    lib().oracle_k_head_norm_rope(_p(kb), _p(w), G, D, rotary_dim, rope_theta, pos, eps)
+    return kb.reshape(G, D)
 
 
 # ------------------------------------------------------ cache semantics --
