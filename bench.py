@@ -144,6 +144,33 @@ def main():
                 mi.attn_step(cache, layer, qs[layer], kn[layer], vn[layer], pos, gate=gs[layer],
                              out=outs[layer])
 
+        # the same step from the f32 projections (norm + RoPE + append + attend
+        # + gate in the same two launches), as the engine would call it
+        qp32 = [torch.randn(H * 2 * D, generator=gen.manual_seed(800 + i), device=dev)
+                for i in range(LAYERS)]
+        k32 = [torch.randn(G * D, generator=gen.manual_seed(900 + i), device=dev)
+               for i in range(LAYERS)]
+        v32 = [torch.randn(G * D, generator=gen.manual_seed(1000 + i), device=dev)
+               for i in range(LAYERS)]
+        qw = (1 + 0.1 * torch.randn(D, generator=gen.manual_seed(1100), device=dev)).bfloat16()
+        kw = (1 + 0.1 * torch.randn(D, generator=gen.manual_seed(1101), device=dev)).bfloat16()
+
+        def proj_step():
+            for layer in range(LAYERS):
+                mi.attn_step_proj(cache, layer, qp32[layer], k32[layer], v32[layer], qw, kw, pos,
+                                  out=outs[layer])
+
+        qo = [torch.empty(H, D, dtype=torch.float16, device=dev) for _ in range(LAYERS)]
+        go = [torch.empty(H, D, dtype=torch.float16, device=dev) for _ in range(LAYERS)]
+
+        def two_call_step():
+            # the same step as two library calls: norm + RoPE + append, then
+            # decode with the gate
+            for layer in range(LAYERS):
+                mi.qk_norm_rope_append(cache, layer, qp32[layer], k32[layer], v32[layer], qw, kw,
+                                       pos, q_out=qo[layer], gate_out=go[layer])
+                mi.attn_decode(cache, layer, qo[layer], C2_CTX, gate=go[layer], out=outs[layer])
+
         def attend_only():
             for layer in range(LAYERS):
                 mi.attn_decode(cache, layer, qs[layer], C2_CTX, gate=gs[layer], out=outs[layer])
@@ -156,15 +183,29 @@ def main():
         ms_attend = timed(attend_only, args.steps, args.warmup,
                           backlog_ms=args.steps * LAYERS * 0.25 + 20)
         _lib.prof_enable(False)
+        ms_proj = timed(proj_step, args.steps, args.warmup,
+                        backlog_ms=args.steps * LAYERS * 0.25 + 20)
+        proj_split_us, _ = _lib.prof_read("attn_split")
+        proj_comb_us, _ = _lib.prof_read("attn_combine")
+        _lib.prof_enable(False)
+        ms_two = timed(two_call_step, args.steps, args.warmup,
+                       backlog_ms=args.steps * LAYERS * 0.35 + 20)
+        rope_us, _ = _lib.prof_read("qk_norm_rope")
+        _lib.prof_enable(False)
         us_layer = ms * 1000 / LAYERS
         rec["decode"] = {
+            "proj_step_us_per_layer": ms_proj * 1000 / LAYERS,
+            "proj_split_kernel_us": proj_split_us, "proj_combine_kernel_us": proj_comb_us,
+            "two_call_step_us_per_layer": ms_two * 1000 / LAYERS, "qk_norm_rope_kernel_us": rope_us,
             "us_per_layer": us_layer, "gbps": C2_BYTES / (us_layer * 1e3),
             "attend_only_us_per_layer": ms_attend * 1000 / LAYERS,
             "split_kernel_us": split_us, "combine_kernel_us": comb_us, "launches": n_split,
             "bytes_per_layer": C2_BYTES, "ms_per_step": ms,
         }
         print(f"[bench] decode step {us_layer:.2f} us/layer (attend only "
-              f"{ms_attend * 100:.2f}) split {split_us:.2f} us combine {comb_us:.2f} us",
+              f"{ms_attend * 100:.2f}, from projections {ms_proj * 100:.2f}: split "
+              f"{proj_split_us:.2f} combine {proj_comb_us:.2f}; two calls {ms_two * 100:.2f}, "
+              f"rope kernel {rope_us:.2f}) split {split_us:.2f} us combine {comb_us:.2f} us",
               file=sys.stderr, flush=True)
         del cache
 

@@ -230,6 +230,23 @@ mi_status mi_qk_norm_rope_append(mi_kv* kv, int32_t layer, const float* q_proj,
                                  int64_t pos, int32_t n, mi_f16* q_out,
                                  mi_f16* gate_out, mi_stream stream);
 
+/* The whole full-attention step of one token from its projections, in the
+ * two kernels of mi_attn_step: Q and K per-head RMS norm + NeoX RoPE at
+ * position pos (as mi_qk_norm_rope_append), append of the rotated K and raw V
+ * at row pos, decode with seq_len = pos + 1 and the sigmoid gate taken from
+ * the gate halves of q_proj.  Replaces q_head_norm_rope, k_head_norm_rope,
+ * kv_cache_append, attn_sdpa_block, attn_sdpa_reduce and sigmoid_gate of
+ * encode_pre_expert_full (src/engine/qwen35_moe/fused_exp2.rs:630-733;
+ * CPU form cpu.rs:126-167).  q_proj: [H][2*D] f32; k, v: [G][D] f32;
+ * weights bf16 [D]; out: [H*D] f16.  rotary_dim must be a multiple of 64
+ * (else MI_ERR_UNSUPPORTED: use mi_qk_norm_rope_append + mi_attn_decode).
+ * len(layer) = pos + 1; pos(kv) is unchanged, as for mi_attn_step. */
+mi_status mi_attn_step_proj(mi_kv* kv, int32_t layer, const float* q_proj,
+                            const float* k, const float* v,
+                            const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                            int32_t rotary_dim, float rope_theta, float eps,
+                            mi_f16* out, int64_t pos, mi_stream stream);
+
 /* ------------------------------------------------------------- profiling -- */
 
 /* Kernel timing with HIP events stamped by each dispatch on its launch

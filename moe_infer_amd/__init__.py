@@ -6,11 +6,12 @@ the C ABI of include/mi_attn.h (libmi_attn.so).  The Python layer mirrors the
 reference engine's Cache / Engine API for this path.
 """
 from . import _lib
-from .attention import (attn_decode, attn_decode_ragged, attn_prefill, attn_step, attn_verify,
-                        kv_cache_append, kv_pack, qk_norm_rope_append, ragged_workspace)
+from .attention import (attn_decode, attn_decode_ragged, attn_prefill, attn_step, attn_step_proj,
+                        attn_verify, kv_cache_append, kv_pack, qk_norm_rope_append,
+                        ragged_workspace)
 from .engine import Engine, EngineSnapshot, record_engine_telemetry
 from .kv_cache import Cache
 
 __all__ = ["Cache", "Engine", "EngineSnapshot", "record_engine_telemetry", "attn_decode",
-           "attn_decode_ragged", "attn_prefill", "attn_step", "attn_verify", "kv_cache_append",
-           "kv_pack", "qk_norm_rope_append", "ragged_workspace", "_lib"]
+           "attn_decode_ragged", "attn_prefill", "attn_step", "attn_step_proj", "attn_verify",
+           "kv_cache_append", "kv_pack", "qk_norm_rope_append", "ragged_workspace", "_lib"]

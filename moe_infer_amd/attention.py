@@ -14,6 +14,8 @@ Reference operators these stand for (fbundle/moe_infer):
                 (src/engine/qwen35_moe/batched.rs:233-260)
   attn_verify   attn_sdpa_causal_n with past_pos = ctx and n = K drafts
   attn_decode_ragged  (no reference counterpart) independent sequences
+  attn_step_proj  the whole step from projections: norm + RoPE + append +
+                attend + gate (src/engine/qwen35_moe/fused_exp2.rs:630-733)
   qk_norm_rope_append  q_head_norm_rope + k_head_norm_rope + kv_cache_append
                 (src/math_util.rs:387-392, 501-593; shaders.metal:2244-2363)
 """
@@ -109,6 +111,30 @@ def qk_norm_rope_append(cache, layer: int, q_proj: torch.Tensor, k: torch.Tensor
         _ptr(k_norm_w), int(rotary_dim), float(rope_theta), float(eps), int(pos), n,
         _ptr(q_out), _ptr(gate_out), _stream()))
     return q_out, gate_out
+
+
+def attn_step_proj(cache, layer: int, q_proj: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                   q_norm_w: torch.Tensor, k_norm_w: torch.Tensor, pos: int,
+                   rotary_dim: int = 64, rope_theta: float = 1e7, eps: float = 1e-6,
+                   out=None) -> torch.Tensor:
+    """One token's full-attention step from its f32 projections (q_proj
+    [H, 2D], k, v [G, D]) and bf16 norm weights: norm + RoPE at `pos`,
+    append at `pos`, decode over pos + 1 rows, sigmoid gate.  Returns
+    [H, D] f16; len(layer) becomes pos + 1."""
+    H, G, D = cache.num_q_heads, cache.num_kv_heads, cache.head_dim
+    _check_tensor("q_proj", q_proj, H * 2 * D, torch.float32)
+    _check_tensor("k", k, G * D, torch.float32)
+    _check_tensor("v", v, G * D, torch.float32)
+    _check_tensor("q_norm_w", q_norm_w, D, torch.bfloat16)
+    _check_tensor("k_norm_w", k_norm_w, D, torch.bfloat16)
+    if out is None:
+        out = torch.empty((H, D), dtype=torch.float16, device=q_proj.device)
+    _check_tensor("out", out, H * D)
+    _lib.check(_lib.lib().mi_attn_step_proj(
+        cache._h, cache.slot(layer), _ptr(q_proj), _ptr(k), _ptr(v), _ptr(q_norm_w),
+        _ptr(k_norm_w), int(rotary_dim), float(rope_theta), float(eps), _ptr(out), int(pos),
+        _stream()))
+    return out
 
 
 def attn_decode(cache, layer: int, q: torch.Tensor, seq_len: int,

@@ -31,6 +31,24 @@ void clear_error();
 // Checks the head shape the kernels are built for.
 mi_status check_shape(int32_t H, int32_t G, int32_t D);
 
+// Q/K head norm + RoPE host side (rope.hip).  Validates the shared
+// arguments of the fused entry points.
+mi_status check_rope(const mi_kv* kv, int32_t rotary_dim, float rope_theta, float eps);
+// rope_theta^(-2i/rotary_dim), i < rotary_dim/2, in f32 as the reference
+// writes it (src/math_util.rs:524).
+void rope_inv_freq(float rope_theta, int32_t rotary_dim, float* inv_freq);
+
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
+// operations, not for its outstanding global loads (which __syncthreads
+// would drain), then synchronises the workgroup.
+__device__ __forceinline__ void sync_lds() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float((uint32_t)b << 16);
+}
+
 // Device layout of the cache (documented in mi_attn.h), in halves.
 // K: 32-row blocks; within a block, row w sits at A-operand row
 // j = 4*(w/8) + w%4 of half u = (w/4)%2, so that a 16-lane group reading

@@ -28,6 +28,9 @@
 //    partial per chunk; attn_combine_kernel merges the chunks, normalises,
 //    applies the sigmoid gate and writes f16.
 #include <cstdlib>
+#include <type_traits>
+
+
 
 #include "common.h"
 
@@ -69,13 +72,127 @@ __device__ __forceinline__ f16x8 load16(const _Float16* p) {
 #endif
 }
 
+// Fused projection input of the decode step (mi_attn_step_proj): the raw
+// q_proj / k / v of one token in f32, normed and rotated inside the split
+// kernel.  cos / sin of the rotation angles pos * inv_freq[i] are computed on
+// the host (the position is a host value), in f32 like the reference:
+// cs[i] = cos, cs[rot_half + i] = sin, i < rot_half.
+struct ProjArgs {
+  const float* q_proj;  // [H][2*D]: query then gate of each head
+  const float* k;       // [G][D]
+  const float* v;       // [G][D]
+  const uint16_t* q_w;  // bf16 [D]
+  const uint16_t* k_w;  // bf16 [D]
+  int rot_half;          // host side: selects the Proj<rot_half / 32> kernel
+  float eps;
+  float cs[MI_ROPE_MAX_DIM];
+};
+struct NoProj {
+  static constexpr int kSH = 0;
+};
+// ProjArgs with the rotation width as a compile-time constant:
+// rot_half = 32 * SH, SH = 0 .. 4.
+template <int SH>
+struct Proj : ProjArgs {
+  static constexpr int kSH = SH;
+};
+template <class X>
+struct is_proj : std::false_type {};
+template <int SH>
+struct is_proj<Proj<SH>> : std::true_type {};
+
+// The 64*SH cos/sin values spread over the wave: entry 64s + lane in tab[s],
+// filled from uniform (scalar) kernel-argument reads.
+template <int SH>
+struct RopeTab {
+  float t[SH > 0 ? SH : 1];
+  __device__ __forceinline__ void fill(const ProjArgs& x, int lane) {
+#pragma unroll
+    for (int s = 0; s < SH; s++) {
+      float v = 0.f;
+#pragma unroll
+      for (int k = 0; k < 64; k++) v = lane == k ? x.cs[64 * s + k] : v;
+      t[s] = v;
+    }
+  }
+  // Entry idx (any lane), read with a cross-lane permute.
+  __device__ __forceinline__ float get(int idx) const {
+    float v = 0.f;
+#pragma unroll
+    for (int s = 0; s < SH; s++) {
+      const float u = __shfl(t[s], idx & 63, 64);
+      v = (idx >> 6) == s ? u : v;
+    }
+    return v;
+  }
+};
+
+// Per-head RMS norm + NeoX rotation, one head per TPH = 256 / DPT adjacent
+// lanes (aligned within the wave): lane index i = lane % TPH holds columns
+// DPT*i .. DPT*i + DPT-1 of the head.  The rotation partner of column
+// d < rot_half, d + rot_half, sits rot_half / DPT lanes up.  Split into the
+// loads (issued early, ahead of the first K/V tile, so that waiting for
+// them does not wait for the tile) and the arithmetic.
+template <int DPT>
+struct HeadPart {
+  float y[DPT];
+  uint32_t wb[DPT / 2];  // bf16 pairs
+  __device__ __forceinline__ void load(const float* src, const uint16_t* w, int lane) {
+    const int i = lane % (D / DPT);
+#pragma unroll
+    for (int e = 0; e < DPT; e += 4) {
+      const float4 f = *(const float4*)(src + DPT * i + e);
+      y[e] = f.x;
+      y[e + 1] = f.y;
+      y[e + 2] = f.z;
+      y[e + 3] = f.w;
+      const uint2 u = *(const uint2*)(w + DPT * i + e);
+      wb[e / 2] = u.x;
+      wb[e / 2 + 1] = u.y;
+    }
+  }
+  template <int SH>
+  __device__ __forceinline__ void norm_rope(const ProjArgs& x, const RopeTab<SH>& tab, int lane) {
+    constexpr int TPH = D / DPT;
+    const int i = lane % TPH;
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < DPT; e++) ss += y[e] * y[e];
+#pragma unroll
+    for (int m = 1; m < TPH; m <<= 1) ss += __shfl_xor(ss, m, 64);
+    const float inv_rms = 1.0f / sqrtf(ss / (float)D + x.eps);
+#pragma unroll
+    for (int e = 0; e < DPT; e++)
+      y[e] = y[e] * inv_rms * mi::bf16_to_f32((uint16_t)(wb[e / 2] >> (16 * (e & 1))));
+    if constexpr (SH > 0) {
+      constexpr int RH = 32 * SH;
+      const int d0 = DPT * i;
+      const bool lower = d0 < RH;
+      const int partner = lower ? lane + RH / DPT : lane - RH / DPT;
+      float pr[DPT];
+#pragma unroll
+      for (int e = 0; e < DPT; e++) pr[e] = __shfl(y[e], partner & 63, 64);
+      const int p0 = lower ? d0 : d0 - RH;
+#pragma unroll
+      for (int e = 0; e < DPT; e++) {
+        const float c = tab.get(p0 + e), sn = tab.get(RH + p0 + e);
+        if (d0 < 2 * RH) y[e] = lower ? y[e] * c - pr[e] * sn : pr[e] * sn + y[e] * c;
+      }
+    }
+  }
+};
+
 // Workgroup = GH KV heads x NWH waves per head, over one chunk of keys of one
 // sequence (with GH = 2 a workgroup reads one contiguous stretch of both
 // heads' K and V blocks).  NCB column blocks of 16 columns (column c = token
 // c / 8, query head c % 8 of the group).
-template <int NWH, int NCB, int GH>
+// With X = ProjArgs (decode step from projections, one token, NCB = 1) the
+// kernel also norms and rotates Q per wave, and the workgroup holding row
+// app0 norms, rotates and appends K and appends V.
+template <int NWH, int NCB, int GH, typename X>
 __global__ void __launch_bounds__(NWH * GH * 64)
-attn_split_kernel(SplitArgs a) {
+attn_split_kernel(SplitArgs a, X x) {
+  constexpr bool kProj = is_proj<X>::value;
   extern __shared__ float smem[];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
@@ -105,7 +222,90 @@ attn_split_kernel(SplitArgs a) {
   if (key_begin >= len) return;  // uniform over the workgroup
   const int64_t key_end = min(key_begin + (int64_t)a.chunk, len);
 
-  if (a.app_n > 0) {
+  // K operand rows: tile u, A-row j <-> key k0 + 8*(j/4) + 4u + j%4, so that
+  // accumulator row 4g+e of tile u is key k0 + 8g + 4u + e.  In the 32-row
+  // block layout this operand (chunk 4kk + g of row j, half u) is one
+  // 16-byte vector, and the 16 lanes of a group read 256 contiguous bytes.
+  // Whole 32-key tiles always lie inside the allocation (cache capacities
+  // are multiples of 256 rows; ragged sequences own whole 32-row blocks),
+  // so the loads are unconditional and straight-line.  Keys past key_end
+  // are masked out of the scores below; their V values are zeroed because
+  // stale rows may hold anything (NaN included) and 0 * NaN is NaN.
+  // V operand: lane (g, j), value block dblk holds V^T[dblk*16 + j][keys
+  // k0+8g .. k0+8g+7] = one 16-byte vector of the block layout.
+  auto load_k = [&](int64_t k0, f16x8(&kf)[2][8]) {
+    const _Float16* kp =
+        a.k + (((row0 + k0) >> 5) * G + kvh) * (int64_t)(32 * D) + g * 128 + j * 8;
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+      for (int kk = 0; kk < 8; kk++) kf[u][kk] = load16(kp + u * (16 * D) + kk * 512);
+  };
+  auto load_v = [&](int64_t k0, f16x8(&vf)[16]) {
+    const _Float16* vp =
+        a.v + (((row0 + k0) >> 3) + g) * G * (int64_t)(D * 8) + kvh * (D * 8) + j * 8;
+#pragma unroll
+    for (int dblk = 0; dblk < 16; dblk++) vf[dblk] = load16(vp + dblk * 128);
+  };
+  // LDS: per KV head of the workgroup the merge area (below); with the
+  // projection prologue then the normed, rotated f16 query rows of the
+  // workgroup's GH*8 heads.
+  constexpr int kLdsRow = D + 4;
+  constexpr int kQRow = D + 8;
+  const int per_head = NWH * ncols * kLdsRow + 3 * NWH * ncols + ncols;
+  _Float16* qs = (_Float16*)(smem + GH * per_head);  // [GH*8][kQRow]
+  // Projection prologue, issue side: this lane's part of the q_proj rows
+  // (one query head per kTPH lanes of the workgroup) is loaded first, then
+  // the first tile's K and V, so the HBM stream starts at once.  The
+  // workgroup that appends row app0 reads its tiles after the append.
+  constexpr int kTPH = NWH * 8;
+  RopeTab<X::kSH> tab;
+  HeadPart<kProj ? D / kTPH : 4> qpart;
+  f16x8 kf[2][8], vf[16];
+  bool peeled = false;
+  const int64_t kfirst = key_begin + 32 * w;
+  if constexpr (kProj) {
+    qpart.load(x.q_proj + ((int64_t)blockIdx.y * GH * 8 + threadIdx.x / kTPH) * (2 * D), x.q_w,
+               lane);
+    tab.fill(x, lane);
+    peeled = !(key_begin <= a.app0 && a.app0 < key_end) && kfirst < key_end;
+    if (peeled) {
+      load_k(kfirst, kf);
+      load_v(kfirst, vf);
+    }
+  }
+
+  if constexpr (kProj) {
+    const int64_t r = a.app0;
+    if (key_begin <= r && r < key_end) {  // workgroup-uniform
+      const int h0 = blockIdx.y * GH;
+      constexpr int TPH = NWH * 8, DPT = D / TPH;
+      if ((int)threadIdx.x < GH * TPH) {  // whole waves
+        // K head h0 + t / TPH, columns DPT * (t % TPH) ...
+        const int hk = threadIdx.x / TPH;
+        HeadPart<DPT> kp;
+        kp.load(x.k + (h0 + hk) * D, x.k_w, lane);
+        kp.template norm_rope<X::kSH>(x, tab, lane);
+        const float(&y)[DPT] = kp.y;
+        if constexpr (DPT == 8) {
+          f16x8 h;
+#pragma unroll
+          for (int e = 0; e < 8; e++) h[e] = (_Float16)y[e];
+          *(f16x8*)(a.kw + mi::k_offset(r, h0 + hk, DPT * (lane % TPH), G, D)) = h;
+        } else {
+          f16x4 h;
+#pragma unroll
+          for (int e = 0; e < 4; e++) h[e] = (_Float16)y[e];
+          *(f16x4*)(a.kw + mi::k_offset(r, h0 + hk, DPT * (lane % TPH), G, D)) = h;
+        }
+      }
+      for (int it = threadIdx.x; it < GH * D; it += NWH * GH * 64) {
+        const int hh = it / D, i = it % D;
+        a.vw[mi::v_offset(r, h0 + hh, i, G, D)] = (_Float16)x.v[(h0 + hh) * D + i];
+      }
+      __syncthreads();  // the row is in L2 before any wave of this group reads it
+    }
+  } else if (a.app_n > 0) {
     // Fused append of the new rows that fall in this chunk, for this
     // workgroup's GH heads; nothing else reads them in this launch.
     const int64_t r_lo = max(key_begin, a.app0);
@@ -128,11 +328,41 @@ attn_split_kernel(SplitArgs a) {
     }
   }
 
+
   // Q^T operand: lane (g, j) holds q[token][head][32kk + 8g + 0..7] for its
   // column j, kk = 0..7 (the column chunk 4kk + g the K operand of the same
   // lane holds).  Padding columns are zero and fully masked.
   f16x8 qf[NCB][8];
   int64_t lim[NCB];
+  if constexpr (kProj) {
+    static_assert(NCB == 1, "projection input is one query token");
+    // Cooperative norm + rotation of the workgroup's GH*8 query heads, one
+    // head per kTPH lanes; the result goes to LDS as f16 and comes back as
+    // this lane's Q^T operand (column j < 8 = query head kvh*8 + j).
+    {
+      constexpr int DPT = D / kTPH;
+      const int hl = threadIdx.x / kTPH;
+      qpart.template norm_rope<X::kSH>(x, tab, lane);
+      _Float16* dst = qs + hl * kQRow + DPT * (lane % kTPH);
+      if constexpr (DPT == 8) {
+        f16x8 h;
+#pragma unroll
+        for (int e = 0; e < 8; e++) h[e] = (_Float16)qpart.y[e];
+        *(f16x8*)dst = h;
+      } else {
+        f16x4 h;
+#pragma unroll
+        for (int e = 0; e < 4; e++) h[e] = (_Float16)qpart.y[e];
+        *(f16x4*)dst = h;
+      }
+    }
+    mi::sync_lds();
+    const bool col = j < 8;
+    const _Float16* qrow = qs + (hw * 8 + (j & 7)) * kQRow + 8 * g;
+#pragma unroll
+    for (int kk = 0; kk < 8; kk++) qf[0][kk] = col ? *(const f16x8*)(qrow + 32 * kk) : f16x8{};
+    lim[0] = col ? a.lim0 : 0;
+  } else {
 #pragma unroll
   for (int cb = 0; cb < NCB; cb++) {
     const int c = cb * 16 + j;
@@ -149,6 +379,7 @@ attn_split_kernel(SplitArgs a) {
       lim[cb] = 0;
     }
   }
+  }
 
   float m[NCB], l[NCB];
   f32x4 acc[NCB][16];
@@ -160,29 +391,11 @@ attn_split_kernel(SplitArgs a) {
     for (int d = 0; d < 16; d++) acc[cb][d] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  for (int64_t k0 = key_begin + 32 * w; k0 < key_end; k0 += 32 * NWH) {
-    // K operand rows: tile u, A-row j <-> key k0 + 8*(j/4) + 4u + j%4, so that
-    // accumulator row 4g+e of tile u is key k0 + 8g + 4u + e.  In the 32-row
-    // block layout this operand (chunk 4kk + g of row j, half u) is one
-    // 16-byte vector, and the 16 lanes of a group read 256 contiguous bytes.
-    const _Float16* kp =
-        a.k + (((row0 + k0) >> 5) * G + kvh) * (int64_t)(32 * D) + g * 128 + j * 8;
-    // Whole 32-key tiles always lie inside the allocation (cache capacities
-    // are multiples of 256 rows; ragged sequences own whole 32-row blocks),
-    // so the loads are unconditional and straight-line.  Keys past key_end
-    // are masked out of the scores below; their V values are zeroed because
-    // stale rows may hold anything (NaN included) and 0 * NaN is NaN.
-    f16x8 kf[2][8];
-#pragma unroll
-    for (int u = 0; u < 2; u++)
-#pragma unroll
-      for (int kk = 0; kk < 8; kk++) kf[u][kk] = load16(kp + u * (16 * D) + kk * 512);
-    // V operand: lane (g, j), value block dblk holds V^T[dblk*16 + j][keys
-    // k0+8g .. k0+8g+7] = one 16-byte vector of the block layout.
-    f16x8 vf[16];
-    const _Float16* vp = a.v + (((row0 + k0) >> 3) + g) * G * (int64_t)(D * 8) + kvh * (D * 8) + j * 8;
-#pragma unroll
-    for (int dblk = 0; dblk < 16; dblk++) vf[dblk] = load16(vp + dblk * 128);
+  for (int64_t k0 = kfirst; k0 < key_end; k0 += 32 * NWH) {
+    if (!peeled || k0 != kfirst) {
+      load_k(k0, kf);
+      load_v(k0, vf);
+    }
     if (k0 + 32 > key_end) {  // the last, partial tile (wave-uniform branch)
       const int64_t valid = key_end - (k0 + 8 * g);
 #pragma unroll
@@ -210,10 +423,10 @@ attn_split_kernel(SplitArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           const int64_t key = k0 + 8 * g + 4 * u + e;
-          float x = st[u][e] * a.scale_log2e;
-          x = (key < lim[cb] && key < key_end) ? x : -INFINITY;
-          st[u][e] = x;
-          mt = fmaxf(mt, x);
+          float sv = st[u][e] * a.scale_log2e;
+          sv = (key < lim[cb] && key < key_end) ? sv : -INFINITY;
+          st[u][e] = sv;
+          mt = fmaxf(mt, sv);
         }
       mt = mi::max_rows(mt);
       const float mnew = fmaxf(m[cb], mt);
@@ -244,8 +457,6 @@ attn_split_kernel(SplitArgs a) {
   // O [NWH][ncols][kLdsRow] (row padded by 4 floats so the 16 columns a
   // lane group writes fall in distinct banks), then m, l [NWH][ncols], then
   // the merge weights 2^(m_w - M) [NWH][ncols] and the merged l [ncols].
-  constexpr int kLdsRow = D + 4;
-  const int per_head = NWH * ncols * kLdsRow + 3 * NWH * ncols + ncols;
   float* so = smem + hw * per_head;
   float* sm = so + NWH * ncols * kLdsRow;
   float* sl = sm + NWH * ncols;
@@ -311,6 +522,7 @@ struct CombineArgs {
   const float* part_o;
   const float* part_ml;
   const _Float16* gate;    // [batch][nq][H][D] or null
+  const float* gate32;     // or the gate halves of q_proj [nq][H][2*D] (else null)
   _Float16* out;           // [batch][nq][H][D]
   int G, H, nq, chunk, max_chunks;
 };
@@ -414,6 +626,10 @@ attn_combine_kernel(CombineArgs a) {
     if (a.gate) {
       const float gv = (float)a.gate[oidx];
       r *= 1.f / (1.f + expf(-gv));
+    } else if (a.gate32) {
+      const float gv =
+          a.gate32[(((int64_t)s * a.nq + tok) * a.H + hq) * (2 * D) + D + d0 + t];
+      r *= 1.f / (1.f + expf(-gv));
     }
     a.out[oidx] = (_Float16)r;
   }
@@ -464,21 +680,30 @@ SplitPlan plan_split(int64_t max_len, int64_t batch, int G, int nq) {
   return p;
 }
 
-template <int NWH, int NCB, int GH>
-mi_status launch_split(const SplitArgs& a, int64_t batch, hipStream_t stream) {
+template <int NWH, int NCB, int GH, typename X = NoProj>
+mi_status launch_split(const SplitArgs& a, int64_t batch, hipStream_t stream, const X& x = X()) {
   const int ncols = a.nq * 8;
-  const size_t lds =
-      (size_t)GH * (NWH * ncols * (D + 4) + 3 * NWH * ncols + ncols) * sizeof(float);
+  size_t lds = (size_t)GH * (NWH * ncols * (D + 4) + 3 * NWH * ncols + ncols) * sizeof(float);
+  if constexpr (is_proj<X>::value) lds += (size_t)GH * 8 * (D + 8) * sizeof(_Float16);
   static bool attr_done = false;
   if (!attr_done) {
-    MI_HIP(hipFuncSetAttribute((const void*)attn_split_kernel<NWH, NCB, GH>,
+    MI_HIP(hipFuncSetAttribute((const void*)attn_split_kernel<NWH, NCB, GH, X>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
     attr_done = true;
   }
   dim3 grid(a.max_chunks, a.G / GH, (unsigned)batch);
-  MI_HIP(mi::launch("attn_split", attn_split_kernel<NWH, NCB, GH>, grid, dim3(NWH * GH * 64),
-                    lds, stream, a));
+  MI_HIP(mi::launch("attn_split", attn_split_kernel<NWH, NCB, GH, X>, grid,
+                    dim3(NWH * GH * 64), lds, stream, a, x));
   return MI_OK;
+}
+
+template <int SH>
+mi_status launch_proj(const SplitArgs& a, const SplitPlan& plan, hipStream_t stream,
+                      const ProjArgs& p) {
+  Proj<SH> x;
+  static_cast<ProjArgs&>(x) = p;
+  if (plan.gh == 2) return launch_split<4, 1, 2>(a, 1, stream, x);
+  return launch_split<8, 1, 1>(a, 1, stream, x);
 }
 
 size_t split_workspace_bytes(int64_t batch, int G, int max_chunks, int nq) {
@@ -499,7 +724,7 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
                     int64_t max_len, int64_t batch, int H, int G, int nq,
                     const _Float16* q, const _Float16* gate, _Float16* out,
                     void* ws, size_t ws_bytes, hipStream_t stream,
-                    const AppendRows& app = AppendRows()) {
+                    const AppendRows& app = AppendRows(), const ProjArgs* proj = nullptr) {
   const SplitPlan plan = plan_split(max_len, batch, G, nq);
   SplitArgs a;
   a.k = k;
@@ -527,7 +752,17 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
   a.part_o = (float*)ws;
   a.part_ml = a.part_o + (size_t)batch * G * a.max_chunks * nq * 8 * D;
   mi_status st;
-  if (plan.ncb == 2)
+  if (proj) {
+    if (nq != 1 || batch != 1) return mi::fail(MI_ERR_INVALID_ARG, "projection input: one token");
+    switch (proj->rot_half / 32) {
+      case 0: st = launch_proj<0>(a, plan, stream, *proj); break;
+      case 1: st = launch_proj<1>(a, plan, stream, *proj); break;
+      case 2: st = launch_proj<2>(a, plan, stream, *proj); break;
+      case 3: st = launch_proj<3>(a, plan, stream, *proj); break;
+      case 4: st = launch_proj<4>(a, plan, stream, *proj); break;
+      default: return mi::fail(MI_ERR_UNSUPPORTED, "rot_half=%d", proj->rot_half);
+    }
+  } else if (plan.ncb == 2)
     st = launch_split<4, 2, 1>(a, batch, stream);
   else if (plan.gh == 2)
     st = launch_split<4, 1, 2>(a, batch, stream);
@@ -541,6 +776,7 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
   c.part_o = a.part_o;
   c.part_ml = a.part_ml;
   c.gate = gate;
+  c.gate32 = proj ? proj->q_proj : nullptr;
   c.out = out;
   c.G = G;
   c.H = H;
@@ -670,4 +906,51 @@ extern "C" mi_status mi_attn_decode_ragged(const mi_f16* k_rows, const mi_f16* v
                    ml, batch, num_q_heads, num_kv_heads, 1, (const _Float16*)q,
                    (const _Float16*)gate, (_Float16*)out, workspace, workspace_bytes,
                    (hipStream_t)stream);
+}
+
+extern "C" mi_status mi_attn_step_proj(mi_kv* kv, int32_t layer, const float* q_proj,
+                                       const float* k, const float* v,
+                                       const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                                       int32_t rotary_dim, float rope_theta, float eps,
+                                       mi_f16* out, int64_t pos, mi_stream stream) {
+  mi::clear_error();
+  MI_TRY(check_layer(kv, layer));
+  if (!q_proj || !k || !v || !q_norm_w || !k_norm_w || !out)
+    return mi::fail(MI_ERR_INVALID_ARG, "null pointer argument");
+  if (pos < 0) return mi::fail(MI_ERR_OUT_OF_RANGE, "pos=%lld", (long long)pos);
+  MI_TRY(mi::check_rope(kv, rotary_dim, rope_theta, eps));
+  if (rotary_dim % 64)
+    return mi::fail(MI_ERR_UNSUPPORTED,
+                    "rotary_dim=%d: the fused step rotates whole 64-column slices; use "
+                    "mi_qk_norm_rope_append + mi_attn_decode",
+                    rotary_dim);
+  if (pos + 1 > kv->cap) MI_TRY(mi_kv_reserve(kv, pos + 1));
+  ProjArgs x{};
+  x.q_proj = q_proj;
+  x.k = k;
+  x.v = v;
+  x.q_w = q_norm_w;
+  x.k_w = k_norm_w;
+  x.rot_half = rotary_dim / 2;
+  x.eps = eps;
+  float inv_freq[MI_ROPE_MAX_DIM / 2];
+  mi::rope_inv_freq(rope_theta, rotary_dim, inv_freq);
+  const float fpos = (float)pos;
+  for (int i = 0; i < x.rot_half; i++) {
+    const float theta = fpos * inv_freq[i];
+    x.cs[i] = cosf(theta);
+    x.cs[x.rot_half + i] = sinf(theta);
+  }
+  const int64_t rows = pos + 1;
+  const SplitPlan plan = plan_split(rows, 1, kv->G, 1);
+  void* ws;
+  MI_TRY(mi::kv_workspace(kv, split_workspace_bytes(1, kv->G, plan.max_chunks, 1), &ws));
+  AppendRows app;
+  app.row0 = pos;
+  app.n = 1;
+  MI_TRY(run_split(kv->k[layer], kv->v[layer], nullptr, nullptr, rows, rows, rows, 1, kv->H,
+                   kv->G, 1, nullptr, nullptr, (_Float16*)out, ws, kv->ws_bytes,
+                   (hipStream_t)stream, app, &x));
+  kv->len[layer] = pos + 1;
+  return MI_OK;
 }

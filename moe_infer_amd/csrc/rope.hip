@@ -38,10 +38,6 @@ struct RopeArgs {
   float inv_freq[kMaxRotHalf];
 };
 
-__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
-  return __uint_as_float((uint32_t)b << 16);
-}
-
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
@@ -68,8 +64,8 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeArgs a) {
   ss = wave_sum(ss);
   const float inv_rms = 1.0f / sqrtf(ss / (float)D + a.eps);
 
-  float y[4] = {x.x * inv_rms * bf16_to_f32(wb.x), x.y * inv_rms * bf16_to_f32(wb.y),
-                x.z * inv_rms * bf16_to_f32(wb.z), x.w * inv_rms * bf16_to_f32(wb.w)};
+  float y[4] = {x.x * inv_rms * mi::bf16_to_f32(wb.x), x.y * inv_rms * mi::bf16_to_f32(wb.y),
+                x.z * inv_rms * mi::bf16_to_f32(wb.z), x.w * inv_rms * mi::bf16_to_f32(wb.w)};
 
   const int rh = a.rot_half;
   const bool lower = c0 < rh;
@@ -114,6 +110,24 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeArgs a) {
 
 }  // namespace
 
+namespace mi {
+
+mi_status check_rope(const mi_kv* kv, int32_t rotary_dim, float rope_theta, float eps) {
+  if (rotary_dim < 0 || rotary_dim % 8 || rotary_dim > kv->D || rotary_dim > MI_ROPE_MAX_DIM)
+    return fail(MI_ERR_INVALID_ARG, "rotary_dim=%d (multiple of 8, at most %d)", rotary_dim,
+                std::min(kv->D, MI_ROPE_MAX_DIM));
+  if (!(eps >= 0.f) || !(rope_theta > 0.f))
+    return fail(MI_ERR_INVALID_ARG, "eps=%g rope_theta=%g", (double)eps, (double)rope_theta);
+  return MI_OK;
+}
+
+void rope_inv_freq(float rope_theta, int32_t rotary_dim, float* inv_freq) {
+  for (int i = 0; i < rotary_dim / 2; i++)
+    inv_freq[i] = powf(rope_theta, -2.0f * (float)i / (float)rotary_dim);
+}
+
+}  // namespace mi
+
 extern "C" mi_status mi_qk_norm_rope_append(mi_kv* kv, int32_t layer, const float* q_proj,
                                             const float* k, const float* v,
                                             const uint16_t* q_norm_w, const uint16_t* k_norm_w,
@@ -128,11 +142,7 @@ extern "C" mi_status mi_qk_norm_rope_append(mi_kv* kv, int32_t layer, const floa
     return mi::fail(MI_ERR_INVALID_ARG, "null pointer");
   if (n <= 0) return mi::fail(MI_ERR_INVALID_ARG, "n=%d", n);
   if (pos < 0) return mi::fail(MI_ERR_OUT_OF_RANGE, "pos=%lld", (long long)pos);
-  if (rotary_dim < 0 || rotary_dim % 8 || rotary_dim > kv->D || rotary_dim > MI_ROPE_MAX_DIM)
-    return mi::fail(MI_ERR_INVALID_ARG, "rotary_dim=%d (multiple of 8, at most %d)", rotary_dim,
-                    std::min(kv->D, MI_ROPE_MAX_DIM));
-  if (!(eps >= 0.f) || !(rope_theta > 0.f))
-    return mi::fail(MI_ERR_INVALID_ARG, "eps=%g rope_theta=%g", (double)eps, (double)rope_theta);
+  MI_TRY(mi::check_rope(kv, rotary_dim, rope_theta, eps));
   if (pos + n > kv->cap) MI_TRY(mi_kv_reserve(kv, pos + n));
 
   RopeArgs a{};
@@ -150,8 +160,7 @@ extern "C" mi_status mi_qk_norm_rope_append(mi_kv* kv, int32_t layer, const floa
   a.G = kv->G;
   a.rot_half = rotary_dim / 2;
   a.eps = eps;
-  for (int i = 0; i < a.rot_half; i++)
-    a.inv_freq[i] = powf(rope_theta, -2.0f * (float)i / (float)rotary_dim);
+  mi::rope_inv_freq(rope_theta, rotary_dim, a.inv_freq);
 
   const int waves = kv->H + kv->G;
   MI_HIP(mi::launch("qk_norm_rope", qk_norm_rope_kernel, dim3(n, (waves + 3) / 4), dim3(256), 0,

@@ -161,3 +161,101 @@ def test_decode_chain_matches_oracle_chain():
                    v.reshape(T, G * D).astype(np.float16), T,
                    gate=q_proj[T - 1, :, D:].astype(np.float16))
     assert_close(out, ref, "norm-rope-append then decode")
+
+
+# ---------------------------------------------- whole step from projections --
+
+def step_proj_reference(q_proj, k, v, qw, kw, prev_k, prev_v, pos, rot=64):
+    """Oracle chain of one step: norm + rope (f32), f16 rounding of q and of
+    the cached rows, decode in f32, sigmoid gate with the f32 gate."""
+    qr, kr = oracle_rows(q_proj[None], k[None], qw, kw, pos, rot)
+    k_rows = np.concatenate([prev_k, kr.reshape(1, G * D).astype(np.float16)])
+    v_rows = np.concatenate([prev_v, v.reshape(1, G * D).astype(np.float16)])
+    att = O.decode(qr[0].astype(np.float16), k_rows, v_rows, pos + 1)
+    return O.sigmoid_gate(att.reshape(-1), q_proj[:, D:].reshape(-1)).reshape(H, D), kr[0]
+
+
+@pytest.mark.parametrize("pos", [0, 1, 31, 32, 1000, 32767])
+def test_step_proj_matches_oracle_chain(pos):
+    from moe_infer_amd import attn_step_proj
+    announce(f"attn_step_proj pos={pos}")
+    rng = np.random.default_rng(100 + pos)
+    q_proj, k, v, qw, kw = inputs(rng, 1)
+    prev_k = rng.standard_normal((pos, G * D)).astype(np.float16)
+    prev_v = rng.standard_normal((pos, G * D)).astype(np.float16)
+    c = Cache(num_layers=1, capacity=pos + 1)
+    if pos:
+        c.upload(0, prev_k, prev_v)
+    out = attn_step_proj(c, 0, torch.from_numpy(q_proj[0]).cuda(), torch.from_numpy(k[0]).cuda(),
+                         torch.from_numpy(v[0]).cuda(), qw.cuda(), kw.cuda(), pos)
+    ref, kref = step_proj_reference(q_proj[0], k[0], v[0], qw, kw, prev_k, prev_v, pos)
+    assert_close(out, ref, f"step_proj pos={pos}")
+    assert c.len(0) == pos + 1
+    kc, vc = c.download(0, rows=1, row0=pos)
+    assert_within_one_ulp(kc, kref.reshape(1, G * D), f"step_proj k row pos={pos}")
+    np.testing.assert_array_equal(vc.view(np.uint16), f16_bits(v[0]).reshape(1, G * D))
+    if pos:
+        k0, v0 = c.download(0, rows=pos, row0=0)
+        np.testing.assert_array_equal(k0, prev_k)
+        np.testing.assert_array_equal(v0, prev_v)
+
+
+@pytest.mark.parametrize("rot", [0, 128, 256])
+def test_step_proj_rotary_dims(rot):
+    from moe_infer_amd import attn_step_proj
+    announce(f"attn_step_proj rot={rot}")
+    rng = np.random.default_rng(rot)
+    pos = 300
+    q_proj, k, v, qw, kw = inputs(rng, 1)
+    prev_k = rng.standard_normal((pos, G * D)).astype(np.float16)
+    prev_v = rng.standard_normal((pos, G * D)).astype(np.float16)
+    c = Cache(num_layers=1, capacity=512)
+    c.upload(0, prev_k, prev_v)
+    out = attn_step_proj(c, 0, torch.from_numpy(q_proj[0]).cuda(), torch.from_numpy(k[0]).cuda(),
+                         torch.from_numpy(v[0]).cuda(), qw.cuda(), kw.cuda(), pos,
+                         rotary_dim=rot)
+    ref, _ = step_proj_reference(q_proj[0], k[0], v[0], qw, kw, prev_k, prev_v, pos, rot)
+    assert_close(out, ref, f"step_proj rot={rot}")
+
+
+def test_step_proj_sequence_equals_two_kernel_route():
+    """40 steps from an empty cache through attn_step_proj against the same
+    40 tokens through mi_qk_norm_rope_append + attn_decode: equal caches
+    (within one f16 ulp: host vs device sin/cos) and outputs within the
+    contract tolerance of the oracle chain at the last step."""
+    from moe_infer_amd import attn_step_proj
+    announce("attn_step_proj sequence")
+    rng = np.random.default_rng(77)
+    T = 40
+    q_proj, k, v, qw, kw = inputs(rng, T)
+    c1 = Cache(num_layers=1, capacity=256)
+    c2 = Cache(num_layers=1, capacity=256)
+    for t in range(T):
+        qp = torch.from_numpy(q_proj[t]).cuda()
+        kt, vt = torch.from_numpy(k[t]).cuda(), torch.from_numpy(v[t]).cuda()
+        out1 = attn_step_proj(c1, 0, qp, kt, vt, qw.cuda(), kw.cuda(), t)
+        q2, g2 = qk_norm_rope_append(c2, 0, qp.reshape(1, H, 2 * D), kt.reshape(1, G, D),
+                                     vt.reshape(1, G, D), qw.cuda(), kw.cuda(), t)
+        out2 = attn_decode(c2, 0, q2[0].contiguous(), t + 1, gate=g2[0].contiguous())
+    k1, v1 = c1.download(0)
+    k2, v2 = c2.download(0)
+    np.testing.assert_array_equal(v1, v2)
+    d = np.abs(k1.astype(np.float64) - k2.astype(np.float64))
+    assert float((d / np.spacing(np.abs(k2))).max()) <= 1.0
+    qr, kr = oracle_rows(q_proj, k, qw, kw, 0)
+    att = O.decode(qr[T - 1].astype(np.float16), kr.reshape(T, G * D).astype(np.float16),
+                   v.reshape(T, G * D).astype(np.float16), T)
+    ref = O.sigmoid_gate(att.reshape(-1), q_proj[T - 1, :, D:].reshape(-1))
+    assert_close(out1, ref, "step_proj sequence last token")
+    assert_close(out2, ref, "two-kernel route last token")
+
+
+def test_step_proj_rejects_partial_slices():
+    from moe_infer_amd import attn_step_proj
+    rng = np.random.default_rng(2)
+    q_proj, k, v, qw, kw = inputs(rng, 1)
+    c = Cache(num_layers=1, capacity=256)
+    with pytest.raises(_lib.MiError):
+        attn_step_proj(c, 0, torch.from_numpy(q_proj[0]).cuda(), torch.from_numpy(k[0]).cuda(),
+                       torch.from_numpy(v[0]).cuda(), qw.cuda(), kw.cuda(), 0, rotary_dim=32)
+    assert c.len(0) == 0
