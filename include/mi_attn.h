@@ -161,7 +161,10 @@ mi_status mi_attn_step(mi_kv* kv, int32_t layer, const mi_f16* q,
  * batched.rs:233-260; kernels kv_cache_append_n + attn_sdpa_causal_n,
  * shaders.metal:2656-2792): append n rows k, v [n][G*D] at past_pos, then
  * query i (q [n][H][D]) attends rows [0, past_pos + i] inclusive; gate
- * [n][H][D] or NULL; out [n][H][D].  MFMA flash-attention kernel. */
+ * [n][H][D] or NULL; out [n][H][D].  MFMA flash-attention kernel.
+ * k = v = NULL: rows [past_pos, past_pos+n) are already in the cache (written
+ * by mi_qk_norm_rope_append or mi_kv_append; len(layer) >= past_pos + n), no
+ * append; len(layer) becomes past_pos + n. */
 mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
                           const mi_f16* k, const mi_f16* v, const mi_f16* gate,
                           mi_f16* out, int64_t past_pos, int32_t n,
@@ -170,7 +173,8 @@ mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
 /* K-token verify for speculative decoding: same contract as mi_attn_prefill
  * (append at past_pos, query i attends [0, past_pos + i]) for small n, run
  * as a split-K HBM-bound kernel over the cache instead of the MFMA prefill
- * tiles.  Rollback afterwards is mi_kv_set_pos. */
+ * tiles.  Rollback afterwards is mi_kv_set_pos.  k = v = NULL as for
+ * mi_attn_prefill. */
 mi_status mi_attn_verify(mi_kv* kv, int32_t layer, const mi_f16* q,
                          const mi_f16* k, const mi_f16* v, const mi_f16* gate,
                          mi_f16* out, int64_t past_pos, int32_t n,

@@ -156,10 +156,13 @@ def attn_step(cache, layer: int, q, k, v, pos: int, gate=None, out=None) -> torc
 
 
 def attn_prefill(cache, layer: int, q, k, v, past_pos: int, gate=None, out=None) -> torch.Tensor:
-    """Causal batched prefill of n = q.shape[0] tokens ([n, H, D])."""
+    """Causal batched prefill of n = q.shape[0] tokens ([n, H, D]).  With
+    k = v = None the rows [past_pos, past_pos + n) are already in the cache
+    (e.g. from qk_norm_rope_append) and are not appended again."""
     n = q.numel() // (cache.num_q_heads * cache.head_dim)
     out = _check_qgo(cache, q, gate, out, n)
-    _check_kv_rows(cache, k, v, n)
+    if k is not None or v is not None:  # None, None: rows already in the cache
+        _check_kv_rows(cache, k, v, n)
     _lib.check(_lib.lib().mi_attn_prefill(cache._h, cache.slot(layer), _ptr(q), _ptr(k),
                                           _ptr(v), _ptr(gate), _ptr(out), int(past_pos), n,
                                           _stream()))
@@ -171,7 +174,8 @@ def attn_verify(cache, layer: int, q, k, v, past_pos: int, gate=None, out=None) 
     kernel (HBM-bound) for small K."""
     n = q.numel() // (cache.num_q_heads * cache.head_dim)
     out = _check_qgo(cache, q, gate, out, n)
-    _check_kv_rows(cache, k, v, n)
+    if k is not None or v is not None:  # None, None: rows already in the cache
+        _check_kv_rows(cache, k, v, n)
     _lib.check(_lib.lib().mi_attn_verify(cache._h, cache.slot(layer), _ptr(q), _ptr(k),
                                          _ptr(v), _ptr(gate), _ptr(out), int(past_pos), n,
                                          _stream()))

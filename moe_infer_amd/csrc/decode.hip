@@ -30,8 +30,6 @@
 #include <cstdlib>
 #include <type_traits>
 
-
-
 #include "common.h"
 
 namespace {
@@ -61,6 +59,17 @@ struct SplitArgs {
   int64_t app0;
   int app_n;
 };
+
+// Partials are consumed once, by the combine kernel: streaming stores
+// (MI_ATTN_TEMPORAL_PARTIALS at build time keeps the default policy).
+template <typename T>
+__device__ __forceinline__ void store_part(T v, T* p) {
+#if defined(MI_ATTN_TEMPORAL_PARTIALS)
+  *p = v;
+#else
+  __builtin_nontemporal_store(v, p);
+#endif
+}
 
 // 16-byte streaming load of K/V: read once per launch, so it is not kept in
 // the caches (MI_ATTN_TEMPORAL_KV=1 at build time keeps the default policy).
@@ -492,8 +501,8 @@ attn_split_kernel(SplitArgs a, X x) {
     }
     const int64_t pb =
         (((int64_t)s * G + blockIdx.y * GH + h2) * a.max_chunks + chunk_idx) * ncols + c;
-    __builtin_nontemporal_store(M, a.part_ml + pb * 2 + 0);
-    __builtin_nontemporal_store(L, a.part_ml + pb * 2 + 1);
+    store_part(M, a.part_ml + pb * 2 + 0);
+    store_part(L, a.part_ml + pb * 2 + 1);
   }
   __syncthreads();
   // merged O, four columns of d per thread
@@ -509,12 +518,10 @@ attn_split_kernel(SplitArgs a, X x) {
       o += *(const f32x4*)(so2 + (ww * ncols + c) * kLdsRow + d4) * sw2[ww * ncols + c];
     const int64_t pb =
         (((int64_t)s * G + blockIdx.y * GH + h2) * a.max_chunks + chunk_idx) * ncols + c;
-    __builtin_nontemporal_store(o, (f32x4*)(a.part_o + pb * D + d4));
+    store_part(o, (f32x4*)(a.part_o + pb * D + d4));
   }
 }
 
-// Partials are written with streaming (non-temporal) stores: they are
-// consumed once, by the next kernel.
 struct CombineArgs {
   const int32_t* offsets;  // ragged (else null)
   const int32_t* lengths;  // ragged (else null)
@@ -868,9 +875,14 @@ extern "C" mi_status mi_attn_verify(mi_kv* kv, int32_t layer, const mi_f16* q,
                                     mi_stream stream) {
   mi::clear_error();
   MI_TRY(check_layer(kv, layer));
-  if (!q || !k || !v || !out) return mi::fail(MI_ERR_INVALID_ARG, "null q/k/v/out");
+  if (!q || !out) return mi::fail(MI_ERR_INVALID_ARG, "null q/out");
+  if (!k != !v) return mi::fail(MI_ERR_INVALID_ARG, "k and v must both be given or both NULL");
   if (n <= 0) return mi::fail(MI_ERR_INVALID_ARG, "n=%d", n);
   if (past_pos < 0) return mi::fail(MI_ERR_OUT_OF_RANGE, "past_pos=%lld", (long long)past_pos);
+  if (!k && past_pos + n > kv->len[layer])
+    return mi::fail(MI_ERR_OUT_OF_RANGE, "k = v = NULL but rows [%lld, %lld) are not in the "
+                    "cache (len %lld)", (long long)past_pos, (long long)(past_pos + n),
+                    (long long)kv->len[layer]);
   if (past_pos + n > kv->cap) MI_TRY(mi_kv_reserve(kv, past_pos + n));
   MI_TRY(cache_attend(kv, layer, (const _Float16*)q, (const _Float16*)gate, (_Float16*)out,
                       past_pos, n, (hipStream_t)stream, (const _Float16*)k, (const _Float16*)v));

@@ -360,14 +360,24 @@ extern "C" mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
   if (!kv) return mi::fail(MI_ERR_INVALID_ARG, "null mi_kv handle");
   if (layer < 0 || layer >= kv->layers)
     return mi::fail(MI_ERR_INVALID_ARG, "layer %d out of [0, %d)", layer, kv->layers);
-  if (!q || !k || !v || !out) return mi::fail(MI_ERR_INVALID_ARG, "null q/k/v/out");
+  if (!q || !out) return mi::fail(MI_ERR_INVALID_ARG, "null q/out");
+  if (!k != !v) return mi::fail(MI_ERR_INVALID_ARG, "k and v must both be given or both NULL");
   if (n <= 0) return mi::fail(MI_ERR_INVALID_ARG, "n=%d", n);
   if (past_pos < 0) return mi::fail(MI_ERR_OUT_OF_RANGE, "past_pos=%lld", (long long)past_pos);
   if (past_pos + n + 2 * BK >= ((int64_t)1 << 31))
     return mi::fail(MI_ERR_OUT_OF_RANGE, "past_pos + n beyond 2^31 rows");
   // Tiles read up to 64 rows past the last key; capacity is a multiple of 256
   // rows, so it suffices that the rows themselves fit.
-  MI_TRY(mi_kv_append(kv, layer, k, v, past_pos, n, stream));
+  if (k) {
+    MI_TRY(mi_kv_append(kv, layer, k, v, past_pos, n, stream));
+  } else {
+    // rows already in the cache (e.g. from mi_qk_norm_rope_append)
+    if (past_pos + n > kv->len[layer])
+      return mi::fail(MI_ERR_OUT_OF_RANGE, "k = v = NULL but rows [%lld, %lld) are not in the "
+                      "cache (len %lld)", (long long)past_pos, (long long)(past_pos + n),
+                      (long long)kv->len[layer]);
+    kv->len[layer] = past_pos + n;
+  }
   hipStream_t s = (hipStream_t)stream;
   PrefillArgs a;
   a.q = (const _Float16*)q;

@@ -259,3 +259,39 @@ def test_step_proj_rejects_partial_slices():
         attn_step_proj(c, 0, torch.from_numpy(q_proj[0]).cuda(), torch.from_numpy(k[0]).cuda(),
                        torch.from_numpy(v[0]).cuda(), qw.cuda(), kw.cuda(), 0, rotary_dim=32)
     assert c.len(0) == 0
+
+
+@pytest.mark.parametrize("past,n", [(0, 200), (37, 130)])
+def test_prefill_over_rope_appended_rows(past, n):
+    """Batched prefill path: norm + RoPE + append of n tokens in one call,
+    then mi_attn_prefill with k = v = NULL over the rows in place; equal to
+    the oracle's norm + RoPE (f16-rounded) followed by its causal attention."""
+    from moe_infer_amd import attn_prefill
+    announce(f"rope -> prefill past={past} n={n}")
+    rng = np.random.default_rng(past + n)
+    q_proj, k, v, qw, kw = inputs(rng, n)
+    prev_k = rng.standard_normal((past, G * D)).astype(np.float16)
+    prev_v = rng.standard_normal((past, G * D)).astype(np.float16)
+    c = Cache(num_layers=1, capacity=past + n)
+    if past:
+        c.upload(0, prev_k, prev_v)
+        c.set_len(0, past)
+    q_out, g_out = qk_norm_rope_append(
+        c, 0, torch.from_numpy(q_proj).cuda(), torch.from_numpy(k).cuda(),
+        torch.from_numpy(v).cuda(), qw.cuda(), kw.cuda(), past)
+    out = attn_prefill(c, 0, q_out, None, None, past, gate=g_out)
+    assert c.len(0) == past + n
+    qr, kr = oracle_rows(q_proj, k, qw, kw, past)
+    k_rows = np.concatenate([prev_k, kr.reshape(n, G * D).astype(np.float16)])
+    v_rows = np.concatenate([prev_v, v.reshape(n, G * D).astype(np.float16)])
+    ref = O.causal(qr.astype(np.float16), k_rows, v_rows, past,
+                   gate=q_proj[:, :, D:].astype(np.float16))
+    assert_close(out, ref, f"rope -> prefill past={past} n={n}")
+
+
+def test_prefill_null_rows_must_be_present():
+    from moe_infer_amd import attn_prefill
+    c = Cache(num_layers=1, capacity=256)
+    q = torch.zeros(4, H, D, dtype=torch.float16, device="cuda")
+    with pytest.raises(_lib.MiValueError):
+        attn_prefill(c, 0, q, None, None, 0)
