@@ -65,11 +65,17 @@ attn_prefill_kernel(PrefillArgs a) {
   const int hl = lane >> 5;   // lane half
   const int col = lane & 31;  // query column of this lane
 
-  // blockIdx -> (query tile, KV head, head in group); 8 heads of one
-  // (tile, KV head) land on one XCD (dispatch is round-robin over 8 XCDs).
+  // blockIdx -> (query tile, KV head, head in group).  Work item li = 8g + h:
+  // group g = (query tile, KV head), heaviest first, h = one of its 8 query
+  // heads.  Dispatch is round-robin over the 8 XCDs (bid % 8), so the 8 heads
+  // of a group go to one XCD and share its L2.  Groups are dealt to the XCDs
+  // in a snake (block j of 8 groups: XCD x takes group 8j + x for even j,
+  // 8j + 7 - x for odd j), so every XCD gets the same causal work; within an
+  // XCD its groups still come heaviest first.
   const int bid = blockIdx.x;
   const int xcd = bid & 7, r = bid >> 3;
-  const int li = (r >> 3) * 64 + xcd * 8 + (r & 7);
+  const int jb = r >> 3;
+  const int li = (8 * jb + ((jb & 1) ? 7 - xcd : xcd)) * 8 + (r & 7);
   if (li >= a.work) return;
   const int hg = li & 7;
   const int kvh = (li >> 3) % a.G;
