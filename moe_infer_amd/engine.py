@@ -10,7 +10,13 @@ per-layer q / k / v / gate projections and get the gated attention output.
                              append at engine_pos, attend [0, pos], gate;
                              then pos += 1 (fused_exp2.rs:989-1039)
   forward_batched(layers)    n tokens per layer, causal (batched.rs:129-312);
-                             pos += n (fused_exp3.rs:291)
+                             pos += n (fused_exp3.rs:291).  n <= VERIFY_MAX_TOKENS
+                             runs the split-K verify kernel (HBM-bound, the
+                             whole cache in one pass per 4 tokens), larger n
+                             the MFMA prefill kernel
+  forward_proj(layers) /     the same two steps from the f32 projections:
+  forward_batched_proj(...)  per-head Q/K RMS norm + NeoX partial RoPE fused in
+                             (cpu.rs:122-145, fused_exp2.rs:630-733)
   mtp_forward(...)           MTP layer: append at mtp_pos, attend, mtp_pos += 1
                              (mtp.rs:143-156, 223)
   mtp_verify(...)            K draft tokens at once (split-K verify kernel)
@@ -44,9 +50,36 @@ class EngineSnapshot:
     mtp_pos: int
 
 
+# Largest token count forward_batched sends to the split-K verify kernel: it
+# reads the cache once per 4 tokens, which beats the prefill kernel (one
+# workgroup per (query tile, head)) when the new tokens are few and the cache
+# is long, the speculative-verify case.
+VERIFY_MAX_TOKENS = 16
+
+
+def _cfg(config, key, default):
+    if config is None:
+        return default
+    if isinstance(config, dict):
+        if key in config:
+            return config[key]
+        tc = config.get("text_config")
+        if isinstance(tc, dict) and key in tc:
+            return tc[key]
+        return default
+    return getattr(config, key, default)
+
+
 class Engine:
-    def __init__(self, cache: Cache, mtp_capacity: int = 4096):
+    def __init__(self, cache: Cache, mtp_capacity: int = 4096, config=None):
+        """config: the model's config.json dict (or None for Qwen3.6's values);
+        rope_theta, partial_rotary_factor and rms_norm_eps feed the
+        projection-input methods (constants.rs:166-167, constants.rs:15)."""
         self.cache = cache
+        hd = cache.head_dim
+        self.rope_theta = float(_cfg(config, "rope_theta", 1e7))
+        self.rotary_dim = int(round(float(_cfg(config, "partial_rotary_factor", 0.25)) * hd))
+        self.rms_norm_eps = float(_cfg(config, "rms_norm_eps", 1e-6))
         self.mtp_cache = Cache(num_layers=1, num_q_heads=cache.num_q_heads,
                                num_kv_heads=cache.num_kv_heads, head_dim=cache.head_dim,
                                capacity=mtp_capacity)
@@ -91,8 +124,57 @@ class Engine:
             n = n_l
             if n == 1:
                 outs.append(attention.attn_step(self.cache, layer, q, k, v, pos, gate=gate))
+            elif n <= VERIFY_MAX_TOKENS:
+                outs.append(attention.attn_verify(self.cache, layer, q, k, v, pos, gate=gate))
             else:
                 outs.append(attention.attn_prefill(self.cache, layer, q, k, v, pos, gate=gate))
+        if n is not None:
+            self.cache.set_pos(pos + n)
+            self.cache.gpu_dirty = True
+        self._record("engine.full_attention_batched_ms", t0)
+        return outs
+
+    # -- the same steps from the projections -------------------------------------
+    def forward_proj(self, layers):
+        """layers: sequence of (layer, q_proj[H,2D] f32, k[G,D] f32, v[G,D] f32,
+        q_norm_w[D] bf16, k_norm_w[D] bf16).  Norm + RoPE at engine_pos, append,
+        attend [0, pos], gate from q_proj; then pos += 1."""
+        t0 = time.perf_counter()
+        pos = self.cache.pos
+        outs = [attention.attn_step_proj(self.cache, layer, qp, k, v, qw, kw, pos,
+                                         rotary_dim=self.rotary_dim, rope_theta=self.rope_theta,
+                                         eps=self.rms_norm_eps)
+                for layer, qp, k, v, qw, kw in layers]
+        self.cache.set_pos(pos + 1)
+        self.cache.gpu_dirty = True
+        self._record("engine.full_attention_ms", t0)
+        return outs
+
+    def forward_batched_proj(self, layers):
+        """layers: sequence of (layer, q_proj[n,H,2D], k[n,G,D], v[n,G,D],
+        q_norm_w, k_norm_w), all f32 but the bf16 weights; token i at
+        position engine_pos + i.  Returns [n,H,D] f16 per layer; pos += n."""
+        t0 = time.perf_counter()
+        pos = self.cache.pos
+        outs, n = [], None
+        H, D = self.cache.num_q_heads, self.cache.head_dim
+        for layer, qp, k, v, qw, kw in layers:
+            n_l = qp.numel() // (H * 2 * D)
+            if n is not None and n_l != n:
+                raise ValueError("every layer must carry the same token count")
+            n = n_l
+            if n == 1:
+                o = attention.attn_step_proj(self.cache, layer, qp, k, v, qw, kw, pos,
+                                             rotary_dim=self.rotary_dim,
+                                             rope_theta=self.rope_theta, eps=self.rms_norm_eps)
+                outs.append(o.reshape(1, H, D))
+                continue
+            q, g = attention.qk_norm_rope_append(self.cache, layer, qp, k, v, qw, kw, pos,
+                                                 rotary_dim=self.rotary_dim,
+                                                 rope_theta=self.rope_theta,
+                                                 eps=self.rms_norm_eps)
+            attend = attention.attn_verify if n <= VERIFY_MAX_TOKENS else attention.attn_prefill
+            outs.append(attend(self.cache, layer, q, None, None, pos, gate=g))
         if n is not None:
             self.cache.set_pos(pos + n)
             self.cache.gpu_dirty = True
