@@ -45,7 +45,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="bounded CPU-baseline sample length")
-    p.add_argument("--only", default="", help="comma list of decode,prefill,verify,ragged")
+    p.add_argument("--only", default="", help="comma list of decode,prefill,verify,ragged,oproj")
     p.add_argument("--copy-calib", action="store_true",
                    help="also run a plain 256 MiB device copy (reference for HBM counters)")
     return p.parse_args()
@@ -291,6 +291,46 @@ def main():
         print(f"[bench] ragged {ms * 1000:.1f} us", file=sys.stderr, flush=True)
         del k, vb  # k holds the packed K blocks
 
+    # ------------------------------------------------- o_proj matvec (bf16, q4)
+    # out[2048] = W[2048, 4096] x[4096] after the gate; enough distinct weight
+    # matrices that the set exceeds the 256 MiB last-level cache, as in a
+    # model step where the layer's weights arrive cold.
+    if not only or "oproj" in only:
+        od, idim, gsz = 2048, H * D, 64
+        nb, nq = 40, 96
+        xs = randn(idim, seed=41)
+        wb = [randn(od, idim, seed=900 + i).to(torch.bfloat16) for i in range(nb)]
+        wq = [torch.randint(-2**31, 2**31 - 1, (od, idim // 8), dtype=torch.int32, device=dev)
+              for _ in range(nq)]
+        sq = torch.full((od, idim // gsz), 0.01, dtype=torch.bfloat16, device=dev)
+        bq = torch.full((od, idim // gsz), -0.07, dtype=torch.bfloat16, device=dev)
+        ob = torch.empty(od, dtype=torch.float32, device=dev)
+
+        def bf16_step():
+            for w in wb:
+                mi.matvec_bf16(xs, w, out=ob)
+
+        def q4_step():
+            for w in wq:
+                mi.matvec_q4(xs, w, sq, bq, group_size=gsz, out=ob)
+
+        ms_b = timed(bf16_step, args.steps, args.warmup, backlog_ms=nb * 0.05 * args.steps + 20)
+        kb_us, _ = _lib.prof_read("matvec_bf16")
+        _lib.prof_enable(False)
+        ms_q = timed(q4_step, args.steps, args.warmup, backlog_ms=nq * 0.02 * args.steps + 20)
+        kq_us, _ = _lib.prof_read("matvec_q4")
+        _lib.prof_enable(False)
+        bytes_b = od * idim * 2 + idim * 2 + od * 4
+        bytes_q = od * idim // 2 + 2 * od * (idim // gsz) * 2 + idim * 2 + od * 4
+        rec["oproj"] = {"bf16_us": ms_b * 1000 / nb, "bf16_kernel_us": kb_us,
+                        "bf16_gbps": bytes_b / (ms_b * 1e6 / nb), "bf16_bytes": bytes_b,
+                        "q4_us": ms_q * 1000 / nq, "q4_kernel_us": kq_us,
+                        "q4_gbps": bytes_q / (ms_q * 1e6 / nq), "q4_bytes": bytes_q,
+                        "shape": [od, idim], "group_size": gsz}
+        print(f"[bench] oproj bf16 {ms_b * 1000 / nb:.2f} us, q4 {ms_q * 1000 / nq:.2f} us",
+              file=sys.stderr, flush=True)
+        del wb, wq
+
     # -------------------------------------------------------------- CPU baseline
     cpu = None
     if (not only or "decode" in only) and args.cpu_seconds > 0:
@@ -360,7 +400,7 @@ def main():
                                     "traffic": traffic_of("prefill_c4")}
         line["prefill"] = {k2: (round(v2, 3) if isinstance(v2, float) else v2)
                            for k2, v2 in p.items()}
-    for key in ("verify", "ragged"):
+    for key in ("verify", "ragged", "oproj"):
         if key in rec:
             line[key] = {k2: (round(v2, 3) if isinstance(v2, float) else v2)
                          for k2, v2 in rec[key].items()}

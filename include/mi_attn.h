@@ -251,6 +251,27 @@ mi_status mi_attn_step_proj(mi_kv* kv, int32_t layer, const float* q_proj,
                             int32_t rotary_dim, float rope_theta, float eps,
                             mi_f16* out, int64_t pos, mi_stream stream);
 
+/* ------------------------------------------------------------- o_proj -- */
+
+/* o_proj of the gated attention output: out[r] = sum_c W[r][c] * x[c] for
+ * r < out_dim, W [out_dim][in_dim] bf16 (bit patterns), x [in_dim] f16 (the
+ * output of mi_attn_decode / mi_attn_step with the gate), out f32.  Replaces
+ * the BF16 matvec of the o_proj (matvec_bf16, src/engine/shaders.metal:
+ * 2392-2425; dispatched at src/engine/qwen35_moe/fused_exp2.rs:732).
+ * in_dim must be a multiple of 512.  Async. */
+mi_status mi_matvec_bf16(const mi_f16* x, const uint16_t* w, float* out,
+                         int32_t out_dim, int32_t in_dim, mi_stream stream);
+
+/* The same with the reference's 4-bit affine weights (dequant_matvec_4bit,
+ * src/math_util.rs:14-57): w_packed [out_dim][in_dim/8] u32, eight nibbles
+ * per word, low nibble first = the lower column; scales, biases bf16
+ * [out_dim][in_dim/group_size]; weight = nibble * scale + bias.  in_dim a
+ * multiple of 2048, group_size a multiple of 32 dividing in_dim.  Async. */
+mi_status mi_matvec_q4(const mi_f16* x, const uint32_t* w_packed,
+                       const uint16_t* scales, const uint16_t* biases,
+                       int32_t group_size, float* out, int32_t out_dim,
+                       int32_t in_dim, mi_stream stream);
+
 /* ------------------------------------------------------------- profiling -- */
 
 /* Kernel timing with HIP events stamped by each dispatch on its launch
@@ -258,7 +279,7 @@ mi_status mi_attn_step_proj(mi_kv* kv, int32_t layer, const float* q_proj,
  * kernel granularity).  mi_prof_enable synchronises the device and clears
  * earlier records.  Kernel names: "attn_split", "attn_combine",
  * "attn_prefill", "kv_pack",
- * "qk_norm_rope".
+ * "qk_norm_rope", "matvec_bf16", "matvec_q4".
  * mi_prof_read returns the mean duration in microseconds and the number of
  * launches recorded since the last enable. */
 void mi_prof_enable(int on);

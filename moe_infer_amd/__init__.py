@@ -7,11 +7,12 @@ reference engine's Cache / Engine API for this path.
 """
 from . import _lib
 from .attention import (attn_decode, attn_decode_ragged, attn_prefill, attn_step, attn_step_proj,
-                        attn_verify, kv_cache_append, kv_pack, qk_norm_rope_append,
-                        ragged_workspace)
+                        attn_verify, kv_cache_append, kv_pack, matvec_bf16, matvec_q4,
+                        qk_norm_rope_append, ragged_workspace)
 from .engine import Engine, EngineSnapshot, record_engine_telemetry
 from .kv_cache import Cache
 
 __all__ = ["Cache", "Engine", "EngineSnapshot", "record_engine_telemetry", "attn_decode",
            "attn_decode_ragged", "attn_prefill", "attn_step", "attn_step_proj", "attn_verify",
-           "kv_cache_append", "kv_pack", "qk_norm_rope_append", "ragged_workspace", "_lib"]
+           "kv_cache_append", "kv_pack", "matvec_bf16", "matvec_q4", "qk_norm_rope_append",
+           "ragged_workspace", "_lib"]

@@ -60,6 +60,8 @@ SIGNATURES = [
     ("mi_qk_norm_rope_append", ST, [P, I32, P, P, P, P, P, I32, C.c_float, C.c_float, I64, I32,
                                     P, P, P]),
     ("mi_attn_step_proj", ST, [P, I32, P, P, P, P, P, I32, C.c_float, C.c_float, P, I64, P]),
+    ("mi_matvec_bf16", ST, [P, P, P, I32, I32, P]),
+    ("mi_matvec_q4", ST, [P, P, P, P, I32, P, I32, I32, P]),
     ("mi_prof_enable", None, [C.c_int]),
     ("mi_prof_read", ST, [C.c_char_p, C.POINTER(C.c_double), C.POINTER(I64)]),
 ]

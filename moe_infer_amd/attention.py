@@ -16,6 +16,8 @@ Reference operators these stand for (fbundle/moe_infer):
   attn_decode_ragged  (no reference counterpart) independent sequences
   attn_step_proj  the whole step from projections: norm + RoPE + append +
                 attend + gate (src/engine/qwen35_moe/fused_exp2.rs:630-733)
+  matvec_bf16 / matvec_q4  o_proj of the gated output: matvec_bf16
+                (shaders.metal:2392-2425), dequant_matvec_4bit (math_util.rs:14-57)
   qk_norm_rope_append  q_head_norm_rope + k_head_norm_rope + kv_cache_append
                 (src/math_util.rs:387-392, 501-593; shaders.metal:2244-2363)
 """
@@ -246,4 +248,44 @@ def attn_decode_ragged(k_blocks: torch.Tensor, v_blocks: torch.Tensor, offsets: 
     _lib.check(_lib.lib().mi_attn_decode_ragged(
         _ptr(k_blocks), _ptr(v_blocks), _ptr(offsets), _ptr(lengths), batch, int(max_len), H, G,
         D, _ptr(q), _ptr(gate), _ptr(out), _ptr(workspace), workspace.numel(), _stream()))
+    return out
+
+
+def matvec_bf16(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """o_proj: out[r] = sum_c w[r, c] * x[c]; x f16 [in], w bf16 [out, in];
+    returns f32 [out]."""
+    if w.dim() != 2:
+        raise ValueError("w must be [out_dim, in_dim]")
+    out_dim, in_dim = w.shape
+    _check_tensor("x", x, in_dim)
+    _check_tensor("w", w, out_dim * in_dim, torch.bfloat16)
+    if out is None:
+        out = torch.empty(out_dim, dtype=torch.float32, device=x.device)
+    _check_tensor("out", out, out_dim, torch.float32)
+    _lib.check(_lib.lib().mi_matvec_bf16(_ptr(x), _ptr(w), _ptr(out), out_dim, in_dim,
+                                         _stream()))
+    return out
+
+
+def matvec_q4(x: torch.Tensor, w_packed: torch.Tensor, scales: torch.Tensor,
+              biases: torch.Tensor, group_size: int = 64,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """o_proj with 4-bit affine weights: w_packed int32/uint32 [out, in/8]
+    (8 nibbles per word, low nibble first), scales / biases bf16
+    [out, in/group_size]; x f16 [in]; returns f32 [out]."""
+    if w_packed.dim() != 2:
+        raise ValueError("w_packed must be [out_dim, in_dim / 8]")
+    out_dim, in_dim = w_packed.shape[0], w_packed.shape[1] * 8
+    _check_tensor("x", x, in_dim)
+    _check_tensor("w_packed", w_packed, out_dim * in_dim // 8, w_packed.dtype)
+    if w_packed.dtype not in (torch.int32, torch.uint32):
+        raise TypeError("w_packed must be int32 or uint32")
+    ng = in_dim // group_size
+    _check_tensor("scales", scales, out_dim * ng, torch.bfloat16)
+    _check_tensor("biases", biases, out_dim * ng, torch.bfloat16)
+    if out is None:
+        out = torch.empty(out_dim, dtype=torch.float32, device=x.device)
+    _check_tensor("out", out, out_dim, torch.float32)
+    _lib.check(_lib.lib().mi_matvec_q4(_ptr(x), _ptr(w_packed), _ptr(scales), _ptr(biases),
+                                       int(group_size), _ptr(out), out_dim, in_dim, _stream()))
     return out

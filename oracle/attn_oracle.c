@@ -437,3 +437,51 @@ ORACLE_API void oracle_k_head_norm_rope(float* k_buf, const uint16_t* k_norm_w,
   }
   free(orig);
 }
+
+/* ----------------------------------------------------- o_proj matvec -- */
+
+/* src/engine/shaders.metal:2392-2425  matvec_bf16: out[r] = sum_c
+ * bf16(W[r][c]) * x[c] (the Metal kernel's per-lane partial sums and
+ * simd_sum are a reordering of this sum; here it runs in column order). */
+ORACLE_API void oracle_matvec_bf16(const uint16_t* w, const float* x, float* out,
+                                   int64_t out_dim, int64_t in_dim) {
+  for (int64_t r = 0; r < out_dim; r++) {
+    float acc = 0.0f;
+    for (int64_t c = 0; c < in_dim; c++) acc += oracle_bf16_to_f32(w[r * in_dim + c]) * x[c];
+    out[r] = acc;
+  }
+}
+
+/* src/math_util.rs:14-57  dequant_matvec_4bit: 8 nibbles per u32 (low nibble
+ * first), w = nibble * scale + bias per group of group_size columns, scales
+ * and biases bf16 [out_dim][in_dim / group_size]. */
+ORACLE_API void oracle_dequant_matvec_4bit(const uint32_t* w_packed, const uint16_t* scales,
+                                           const uint16_t* biases, const float* x, float* out,
+                                           int64_t out_dim, int64_t in_dim,
+                                           int64_t group_size) {
+  int64_t num_groups = in_dim / group_size;
+  int64_t packed_per_group = group_size / 8;
+  int64_t packed_cols = in_dim / 8;
+  for (int64_t row = 0; row < out_dim; row++) {
+    float acc = 0.0f;
+    const uint32_t* w_row = w_packed + row * packed_cols;
+    const uint16_t* s_row = scales + row * num_groups;
+    const uint16_t* b_row = biases + row * num_groups;
+    for (int64_t g = 0; g < num_groups; g++) {
+      float scale = oracle_bf16_to_f32(s_row[g]);
+      float bias = oracle_bf16_to_f32(b_row[g]);
+      int64_t base_packed = g * packed_per_group;
+      int64_t base_x = g * group_size;
+      for (int64_t p = 0; p < packed_per_group; p++) {
+        uint32_t packed = w_row[base_packed + p];
+        int64_t x_base = base_x + p * 8;
+        for (int n = 0; n < 8; n++) {
+          uint32_t nibble = (packed >> (n * 4)) & 0xFu;
+          float w_val = (float)nibble * scale + bias;
+          acc += w_val * x[x_base + n];
+        }
+      }
+    }
+    out[row] = acc;
+  }
+}

@@ -56,6 +56,8 @@ def lib() -> C.CDLL:
             "oracle_q_head_norm_rope": (None, [P, P, P, P, I64, I64, I64, C.c_float, I64,
                                                C.c_float]),
             "oracle_k_head_norm_rope": (None, [P, P, I64, I64, I64, C.c_float, I64, C.c_float]),
+            "oracle_matvec_bf16": (None, [P, P, P, I64, I64]),
+            "oracle_dequant_matvec_4bit": (None, [P, P, P, P, P, I64, I64, I64]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -225,6 +227,30 @@ def k_head_norm_rope(k, k_norm_w, pos, G=2, D=256, rotary_dim=64, rope_theta=1e7
     w = np.ascontiguousarray(k_norm_w, dtype=np.uint16)
     lib().oracle_k_head_norm_rope(_p(kb), _p(w), G, D, rotary_dim, rope_theta, pos, eps)
     return kb.reshape(G, D)
+
+
+# ------------------------------------------------------ o_proj matvec --
+
+def matvec_bf16(w_bits, x):
+    """w_bits: uint16 bf16 patterns [out, in]; x float [in] -> f32 [out]."""
+    w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    xx = _f(x)
+    out = np.empty(w.shape[0], np.float32)
+    lib().oracle_matvec_bf16(_p(w), _p(xx), _p(out), w.shape[0], w.shape[1])
+    return out
+
+
+def dequant_matvec_4bit(w_packed, scales, biases, x, group_size=64):
+    """w_packed uint32 [out, in/8]; scales, biases bf16 bits [out, in/gs]."""
+    wp = np.ascontiguousarray(w_packed, dtype=np.uint32)
+    sc = np.ascontiguousarray(scales, dtype=np.uint16)
+    bi = np.ascontiguousarray(biases, dtype=np.uint16)
+    xx = _f(x)
+    out_dim, in_dim = wp.shape[0], wp.shape[1] * 8
+    out = np.empty(out_dim, np.float32)
+    lib().oracle_dequant_matvec_4bit(_p(wp), _p(sc), _p(bi), _p(xx), _p(out), out_dim, in_dim,
+                                     group_size)
+    return out
 
 
 # ------------------------------------------------------ cache semantics --
