@@ -22,8 +22,6 @@ namespace {
 constexpr int kRowsPerWave = 2;
 constexpr int kWaves = 4;
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
 __device__ __forceinline__ u32x4 load_nt(const void* p) {
   return __builtin_nontemporal_load((const u32x4*)p);
 }

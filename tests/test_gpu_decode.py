@@ -94,7 +94,7 @@ def test_engine_step_sequence():
 
 
 @pytest.mark.parametrize("n,past", [(1, 0), (2, 5), (3, 31), (4, 61), (4, 255), (7, 100),
-                                    (9, 1000)])
+                                    (9, 1000), (6, 20000)])
 def test_verify_matches_causal_oracle(n, past):
     announce(f"verify n={n} past={past}")
     rng = np.random.default_rng(1000 * n + past)
@@ -135,3 +135,34 @@ def test_verify_c5_and_rollback():
     assert np.array_equal(kd[P + 2].view(np.uint16), k2.view(np.uint16))
     assert np.array_equal(kd[P + 3].view(np.uint16), k[3].view(np.uint16))  # stale, untouched
     assert np.array_equal(vd[:P + 2].view(np.uint16), vall[:P + 2].view(np.uint16))
+
+
+@pytest.mark.parametrize("L", [8193, 40000])
+def test_decode_long_contexts(L):
+    """Chunkings past the 128-key minimum (chunk 256 at 40000 rows)."""
+    announce(f"decode L={L}")
+    rng = np.random.default_rng(L)
+    q, k, v, g = f16(rng, H * D), f16(rng, L, G * D), f16(rng, L, G * D), f16(rng, H * D)
+    c = filled_cache(k, v)
+    out = attn_decode(c, 0, dev(q), L, gate=dev(g))
+    assert_close(out, O.decode(q, k, v, L, gate=g), f"decode L={L}")
+
+
+def test_step_sequence_long_context():
+    """The engine step (append fused into the split kernel) over 200 tokens
+    past 8050 rows, where the number of chunks passes 64."""
+    announce("step sequence at 8K")
+    rng = np.random.default_rng(12)
+    P = 8050
+    kp, vp = f16(rng, P, G * D), f16(rng, P, G * D)
+    c = filled_cache(kp, vp, capacity=P + 300)
+    ks, vs = [kp], [vp]
+    for t in range(P, P + 200):
+        q, g, kn, vn = f16(rng, H * D), f16(rng, H * D), f16(rng, G * D), f16(rng, G * D)
+        out = attn_step(c, 0, dev(q), dev(kn), dev(vn), t, gate=dev(g))
+        ks.append(kn[None])
+        vs.append(vn[None])
+        c.set_pos(t + 1)
+        if t % 50 == 0 or t == P + 199:
+            assert_close(out, O.decode(q, np.concatenate(ks), np.concatenate(vs), t + 1, gate=g),
+                         f"step t={t}")
