@@ -2,6 +2,7 @@
 append / upload / download bit-exactness, position-only rollback, reset,
 doubling growth, copy_from and save/load (src/cache.rs semantics, modelled
 by oracle.CacheModel)."""
+import json
 import numpy as np
 import pytest
 import torch
@@ -177,3 +178,68 @@ def test_copy_from_and_save_load(tmp_path):
         for i in range(2):
             assert np.array_equal(a[i].view(np.uint16), b[i].view(np.uint16))
             assert np.array_equal(a[i].view(np.uint16), x[i].view(np.uint16))
+
+
+def _write_reference_cache(bin_p, json_p, n_layers, full, rows, kv_dim, k, v, lens, pos):
+    """A cache file in the reference's layout (cache.rs:133-177, 236-270):
+    per layer in order either k_cache / v_cache float32 [rows, kv_dim] + len
+    uint32, or the linear layer's conv_state / ssm_state float32; cache.pos
+    last; native-endian; offsets in a JSON manifest."""
+    tensors, off = {}, 0
+    with open(bin_p, "wb") as f:
+        def put(name, arr, shape, dtype):
+            nonlocal off
+            b = arr.tobytes()
+            f.write(b)
+            tensors[name] = {"offset": off, "size": len(b), "shape": shape, "dtype": dtype}
+            off += len(b)
+        for i in range(n_layers):
+            if i in full:
+                put(f"cache.layer_{i}.k_cache", k[i].astype(np.float32), [rows, kv_dim], "float32")
+                put(f"cache.layer_{i}.v_cache", v[i].astype(np.float32), [rows, kv_dim], "float32")
+                put(f"cache.layer_{i}.len", np.array([lens[i]], np.uint32), [], "uint32")
+            else:
+                put(f"cache.layer_{i}.conv_state", np.full((3, 8), 7.0, np.float32), [3, 8],
+                    "float32")
+                put(f"cache.layer_{i}.ssm_state", np.full(16, -3.0, np.float32), [16], "float32")
+        put("cache.pos", np.array([pos], np.uint32), [], "uint32")
+    with open(json_p, "w") as f:
+        json.dump({"tensors": tensors}, f, indent=2)
+
+
+def test_load_reference_float32_file(tmp_path):
+    """A file in the reference's float32 layout, with the linear layers' state
+    in between, loads into the f16 cache: rows are the f16 rounding of the f32
+    values, len per layer and pos as stored; saving writes float16 with the
+    same names, shapes and order, and loads back bit for bit."""
+    rng = np.random.default_rng(15)
+    cfg = {"num_hidden_layers": 8, "num_attention_heads": 16, "num_key_value_heads": 2,
+           "head_dim": 256, "linear_num_value_heads": 32, "linear_num_key_heads": 16}
+    rows, kv_dim, full = 256, G * D, [3, 7]
+    k = {i: rng.standard_normal((rows, kv_dim)).astype(np.float32) for i in full}
+    v = {i: rng.standard_normal((rows, kv_dim)).astype(np.float32) for i in full}
+    lens = {3: 100, 7: 101}
+    bin_p, json_p = str(tmp_path / "ref.bin"), str(tmp_path / "ref.json")
+    _write_reference_cache(bin_p, json_p, 8, full, rows, kv_dim, k, v, lens, 100)
+    c = Cache.load(bin_p, json_p, cfg)
+    assert c.pos == 100 and c.len(3) == 100 and c.len(7) == 101
+    for i in full:
+        kd, vd = c.download(i, rows=rows)
+        assert np.array_equal(kd.view(np.uint16), k[i].astype(np.float16).view(np.uint16))
+        assert np.array_equal(vd.view(np.uint16), v[i].astype(np.float16).view(np.uint16))
+    out_bin, out_json = str(tmp_path / "f16.bin"), str(tmp_path / "f16.json")
+    c.save(out_bin, out_json)
+    with open(out_json) as f:
+        man = json.load(f)["tensors"]
+    names = sorted(man, key=lambda n: man[n]["offset"])
+    assert names == ["cache.layer_3.k_cache", "cache.layer_3.v_cache", "cache.layer_3.len",
+                     "cache.layer_7.k_cache", "cache.layer_7.v_cache", "cache.layer_7.len",
+                     "cache.pos"]
+    assert man["cache.layer_3.k_cache"]["dtype"] == "float16"
+    assert man["cache.layer_3.k_cache"]["shape"] == [c.capacity, kv_dim]
+    e = Cache.load(out_bin, out_json, cfg)
+    assert e.pos == 100 and e.len(7) == 101
+    for i in full:
+        a, b = c.download(i, rows=rows), e.download(i, rows=rows)
+        assert np.array_equal(a[0].view(np.uint16), b[0].view(np.uint16))
+        assert np.array_equal(a[1].view(np.uint16), b[1].view(np.uint16))
