@@ -404,6 +404,13 @@ def main():
         if key in rec:
             line[key] = {k2: (round(v2, 3) if isinstance(v2, float) else v2)
                          for k2, v2 in rec[key].items()}
+    o = rec.get("oproj")
+    if o:
+        ach = o["bf16_bytes"] / (o["bf16_kernel_us"] * 1e3)
+        line["roofline_oproj"] = {"bound": "hbm", "kernel": "matvec_bf16_kernel (o_proj 2048x4096)",
+                                  "achieved": round(ach, 1), "peak": hbm_peak, "unit": "GB/s",
+                                  "frac": round(ach / hbm_peak, 4),
+                                  "traffic": traffic_of("oproj_bf16")}
     line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
 
