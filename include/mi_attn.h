@@ -13,6 +13,9 @@
  *     NULL is the legacy default stream) and is asynchronous unless the name
  *     ends in _sync.  A handle is not internally synchronised: use one handle
  *     per thread (the reference's pyclasses are `unsendable`).
+ *   - A handle belongs to the device that is current at mi_kv_create; calls
+ *     that allocate or launch work on it return MI_ERR_INVALID_ARG unless
+ *     that device is current.
  *   - Shapes: H query heads, G KV heads, head dim D.  The kernels are built
  *     for the Qwen3.6 full-attention shape D = 256, H / G = 8; other shapes
  *     return MI_ERR_UNSUPPORTED.  Softmax scale is 1/sqrt(D), accumulation f32.

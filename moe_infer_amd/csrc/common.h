@@ -6,6 +6,7 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 #include <vector>
 
@@ -17,6 +18,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// MI_HIP for use inside namespace mi before the macros below.
+#define MI_HIP_RAW(call)                                        \
+  do {                                                          \
+    hipError_t e_ = (call);                                     \
+    if (e_ != hipSuccess) return mi::hip_status(e_, #call);     \
+  } while (0)
 
 namespace mi {
 
@@ -90,6 +98,19 @@ __device__ __forceinline__ float sum_rows(float x) {  // sum over lanes l, l^16,
   return sum_xor32(__uint_as_float(r[0]) + __uint_as_float(r[1]));
 }
 
+// Raises `kernel`'s dynamic LDS limit to `bytes` on the current device, once
+// per device (the attribute is held per device); `done` is the kernel's
+// bitmask of devices already set.
+inline mi_status set_lds_limit(const void* kernel, int bytes, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  MI_HIP_RAW(hipGetDevice(&dev));
+  const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return MI_OK;
+  MI_HIP_RAW(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
+  done.fetch_or(bit, std::memory_order_release);
+  return MI_OK;
+}
+
 // Timing event pair for one launch when profiling is on (mi_prof_enable),
 // else two nulls.
 void prof_events(const char* name, hipEvent_t* start, hipEvent_t* stop);
@@ -133,6 +154,11 @@ struct mi_kv {
 };
 
 namespace mi {
+// A non-null handle whose device is the current one (a handle's buffers and
+// launches belong to the device that was current at mi_kv_create).
+mi_status check_kv(const mi_kv* kv);
+// check_kv and 0 <= layer < layers.
+mi_status check_layer(const mi_kv* kv, int32_t layer);
 // Ensures the handle's workspace holds at least `bytes` (synchronous grow).
 mi_status kv_workspace(mi_kv* kv, size_t bytes, void** ws);
 // Enqueues the row copy of kv_cache_append_n on `stream` (no len update).

@@ -692,12 +692,8 @@ mi_status launch_split(const SplitArgs& a, int64_t batch, hipStream_t stream, co
   const int ncols = a.nq * 8;
   size_t lds = (size_t)GH * (NWH * ncols * (D + 4) + 3 * NWH * ncols + ncols) * sizeof(float);
   if constexpr (is_proj<X>::value) lds += (size_t)GH * 8 * (D + 8) * sizeof(_Float16);
-  static bool attr_done = false;
-  if (!attr_done) {
-    MI_HIP(hipFuncSetAttribute((const void*)attn_split_kernel<NWH, NCB, GH, X>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    attr_done = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};
+  MI_TRY(mi::set_lds_limit((const void*)attn_split_kernel<NWH, NCB, GH, X>, 160 * 1024, lds_set));
   dim3 grid(a.max_chunks, a.G / GH, (unsigned)batch);
   MI_HIP(mi::launch("attn_split", attn_split_kernel<NWH, NCB, GH, X>, grid,
                     dim3(NWH * GH * 64), lds, stream, a, x));
@@ -795,13 +791,6 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
   return MI_OK;
 }
 
-mi_status check_layer(const mi_kv* kv, int32_t layer) {
-  if (!kv) return mi::fail(MI_ERR_INVALID_ARG, "null mi_kv handle");
-  if (layer < 0 || layer >= kv->layers)
-    return mi::fail(MI_ERR_INVALID_ARG, "layer %d out of [0, %d)", layer, kv->layers);
-  return MI_OK;
-}
-
 // Verify / decode over the cache: n query tokens at positions past_pos ..
 // past_pos+n-1, rows [0, past_pos+n) already in the cache.
 // With k_new / v_new, the n new rows [past_pos, past_pos + n) are appended
@@ -845,7 +834,7 @@ extern "C" mi_status mi_attn_decode(mi_kv* kv, int32_t layer, const mi_f16* q,
                                     const mi_f16* gate, mi_f16* out, int64_t seq_len,
                                     mi_stream stream) {
   mi::clear_error();
-  MI_TRY(check_layer(kv, layer));
+  MI_TRY(mi::check_layer(kv, layer));
   if (!q || !out) return mi::fail(MI_ERR_INVALID_ARG, "null q/out");
   if (seq_len < 0 || seq_len > kv->cap)
     return mi::fail(MI_ERR_OUT_OF_RANGE, "seq_len %lld outside [0, capacity %lld]",
@@ -859,7 +848,7 @@ extern "C" mi_status mi_attn_step(mi_kv* kv, int32_t layer, const mi_f16* q,
                                   const mi_f16* k, const mi_f16* v, const mi_f16* gate,
                                   mi_f16* out, int64_t pos, mi_stream stream) {
   mi::clear_error();
-  MI_TRY(check_layer(kv, layer));
+  MI_TRY(mi::check_layer(kv, layer));
   if (!q || !k || !v || !out) return mi::fail(MI_ERR_INVALID_ARG, "null q/k/v/out");
   if (pos < 0) return mi::fail(MI_ERR_OUT_OF_RANGE, "pos=%lld", (long long)pos);
   if (pos + 1 > kv->cap) MI_TRY(mi_kv_reserve(kv, pos + 1));
@@ -874,7 +863,7 @@ extern "C" mi_status mi_attn_verify(mi_kv* kv, int32_t layer, const mi_f16* q,
                                     mi_f16* out, int64_t past_pos, int32_t n,
                                     mi_stream stream) {
   mi::clear_error();
-  MI_TRY(check_layer(kv, layer));
+  MI_TRY(mi::check_layer(kv, layer));
   if (!q || !out) return mi::fail(MI_ERR_INVALID_ARG, "null q/out");
   if (!k != !v) return mi::fail(MI_ERR_INVALID_ARG, "k and v must both be given or both NULL");
   if (n <= 0) return mi::fail(MI_ERR_INVALID_ARG, "n=%d", n);
@@ -926,7 +915,7 @@ extern "C" mi_status mi_attn_step_proj(mi_kv* kv, int32_t layer, const float* q_
                                        int32_t rotary_dim, float rope_theta, float eps,
                                        mi_f16* out, int64_t pos, mi_stream stream) {
   mi::clear_error();
-  MI_TRY(check_layer(kv, layer));
+  MI_TRY(mi::check_layer(kv, layer));
   if (!q_proj || !k || !v || !q_norm_w || !k_norm_w || !out)
     return mi::fail(MI_ERR_INVALID_ARG, "null pointer argument");
   if (pos < 0) return mi::fail(MI_ERR_OUT_OF_RANGE, "pos=%lld", (long long)pos);

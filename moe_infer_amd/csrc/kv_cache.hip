@@ -134,15 +134,16 @@ int64_t round_cap(int64_t rows) {
   return (rows + MI_KV_CAP_ALIGN - 1) / MI_KV_CAP_ALIGN * MI_KV_CAP_ALIGN;
 }
 
-size_t layer_bytes(const mi_kv* kv, int64_t cap) {
-  return (size_t)cap * kv->G * kv->D * sizeof(_Float16);
-}
-
-mi_status check_layer(const mi_kv* kv, int32_t layer) {
+// Host-state queries: a non-null handle and a layer in range (no device).
+mi_status layer_in_range(const mi_kv* kv, int32_t layer) {
   if (!kv) return mi::fail(MI_ERR_INVALID_ARG, "null mi_kv handle");
   if (layer < 0 || layer >= kv->layers)
     return mi::fail(MI_ERR_INVALID_ARG, "layer %d out of [0, %d)", layer, kv->layers);
   return MI_OK;
+}
+
+size_t layer_bytes(const mi_kv* kv, int64_t cap) {
+  return (size_t)cap * kv->G * kv->D * sizeof(_Float16);
 }
 
 void free_layers(mi_kv* kv) {
@@ -186,6 +187,23 @@ mi_status realloc_layers(mi_kv* kv, int64_t cap, int64_t keep_rows) {
 }  // namespace
 
 namespace mi {
+
+mi_status check_kv(const mi_kv* kv) {
+  if (!kv) return mi::fail(MI_ERR_INVALID_ARG, "null mi_kv handle");
+  int dev = 0;
+  MI_HIP(hipGetDevice(&dev));
+  if (dev != kv->device)
+    return mi::fail(MI_ERR_INVALID_ARG, "the handle belongs to device %d; device %d is current",
+                    kv->device, dev);
+  return MI_OK;
+}
+
+mi_status check_layer(const mi_kv* kv, int32_t layer) {
+  MI_TRY(check_kv(kv));
+  if (layer < 0 || layer >= kv->layers)
+    return mi::fail(MI_ERR_INVALID_ARG, "layer %d out of [0, %d)", layer, kv->layers);
+  return MI_OK;
+}
 
 mi_status kv_workspace(mi_kv* kv, size_t bytes, void** ws) {
   if (bytes > kv->ws_bytes) {
@@ -258,7 +276,7 @@ extern "C" void mi_kv_destroy(mi_kv* kv) {
 
 extern "C" mi_status mi_kv_reserve(mi_kv* kv, int64_t capacity) {
   mi::clear_error();
-  if (!kv) return mi::fail(MI_ERR_INVALID_ARG, "null mi_kv handle");
+  MI_TRY(mi::check_kv(kv));
   if (capacity <= kv->cap) return MI_OK;
   // Doubling growth (metal_context.rs:368-431), at least to `capacity`.
   int64_t cap = kv->cap;
@@ -303,14 +321,14 @@ extern "C" mi_status mi_kv_pos(const mi_kv* kv, int64_t* pos) {
 }
 
 extern "C" mi_status mi_kv_len(const mi_kv* kv, int32_t layer, int64_t* len) {
-  MI_TRY(check_layer(kv, layer));
+  MI_TRY(layer_in_range(kv, layer));
   if (!len) return mi::fail(MI_ERR_INVALID_ARG, "null argument");
   *len = kv->len[layer];
   return MI_OK;
 }
 
 extern "C" mi_status mi_kv_set_len(mi_kv* kv, int32_t layer, int64_t len) {
-  MI_TRY(check_layer(kv, layer));
+  MI_TRY(layer_in_range(kv, layer));
   if (len < 0 || len > kv->cap)
     return mi::fail(MI_ERR_OUT_OF_RANGE, "len %lld outside [0, capacity %lld]",
                     (long long)len, (long long)kv->cap);
@@ -320,7 +338,7 @@ extern "C" mi_status mi_kv_set_len(mi_kv* kv, int32_t layer, int64_t len) {
 
 extern "C" mi_status mi_kv_layer_ptrs(mi_kv* kv, int32_t layer, mi_f16** k,
                                       mi_f16** v) {
-  MI_TRY(check_layer(kv, layer));
+  MI_TRY(mi::check_layer(kv, layer));
   if (k) *k = (mi_f16*)kv->k[layer];
   if (v) *v = (mi_f16*)kv->v[layer];
   return MI_OK;
@@ -330,7 +348,7 @@ extern "C" mi_status mi_kv_append(mi_kv* kv, int32_t layer, const mi_f16* k,
                                   const mi_f16* v, int64_t pos, int32_t n,
                                   mi_stream stream) {
   mi::clear_error();
-  MI_TRY(check_layer(kv, layer));
+  MI_TRY(mi::check_layer(kv, layer));
   if (!k || !v) return mi::fail(MI_ERR_INVALID_ARG, "null k/v");
   if (n <= 0) return mi::fail(MI_ERR_INVALID_ARG, "n=%d", n);
   if (pos < 0) return mi::fail(MI_ERR_OUT_OF_RANGE, "pos=%lld", (long long)pos);
@@ -398,7 +416,7 @@ mi_status check_rows(const mi_kv* kv, int64_t row0, int64_t rows) {
 extern "C" mi_status mi_kv_upload(mi_kv* kv, int32_t layer, const mi_f16* host_k,
                                   const mi_f16* host_v, int64_t row0, int64_t rows) {
   mi::clear_error();
-  MI_TRY(check_layer(kv, layer));
+  MI_TRY(mi::check_layer(kv, layer));
   if (!host_k || !host_v) return mi::fail(MI_ERR_INVALID_ARG, "null host buffer");
   MI_TRY(check_rows(kv, row0, rows));
   if (rows == 0) return MI_OK;
@@ -424,7 +442,7 @@ extern "C" mi_status mi_kv_upload(mi_kv* kv, int32_t layer, const mi_f16* host_k
 extern "C" mi_status mi_kv_download(const mi_kv* kv, int32_t layer, mi_f16* host_k,
                                     mi_f16* host_v, int64_t row0, int64_t rows) {
   mi::clear_error();
-  MI_TRY(check_layer(kv, layer));
+  MI_TRY(mi::check_layer(kv, layer));
   if (!host_k || !host_v) return mi::fail(MI_ERR_INVALID_ARG, "null host buffer");
   MI_TRY(check_rows(kv, row0, rows));
   if (rows == 0) return MI_OK;
@@ -445,7 +463,8 @@ extern "C" mi_status mi_kv_download(const mi_kv* kv, int32_t layer, mi_f16* host
 
 extern "C" mi_status mi_kv_copy_from(mi_kv* dst, const mi_kv* src) {
   mi::clear_error();
-  if (!dst || !src) return mi::fail(MI_ERR_INVALID_ARG, "null mi_kv handle");
+  MI_TRY(mi::check_kv(dst));
+  MI_TRY(mi::check_kv(src));
   if (dst->layers != src->layers || dst->H != src->H || dst->G != src->G || dst->D != src->D)
     return mi::fail(MI_ERR_INVALID_ARG, "cache shape mismatch");
   if (dst == src) return MI_OK;

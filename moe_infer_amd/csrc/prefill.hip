@@ -363,9 +363,7 @@ extern "C" mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
                                      mi_f16* out, int64_t past_pos, int32_t n,
                                      mi_stream stream) {
   mi::clear_error();
-  if (!kv) return mi::fail(MI_ERR_INVALID_ARG, "null mi_kv handle");
-  if (layer < 0 || layer >= kv->layers)
-    return mi::fail(MI_ERR_INVALID_ARG, "layer %d out of [0, %d)", layer, kv->layers);
+  MI_TRY(mi::check_layer(kv, layer));
   if (!q || !out) return mi::fail(MI_ERR_INVALID_ARG, "null q/out");
   if (!k != !v) return mi::fail(MI_ERR_INVALID_ARG, "k and v must both be given or both NULL");
   if (n <= 0) return mi::fail(MI_ERR_INVALID_ARG, "n=%d", n);
@@ -398,13 +396,9 @@ extern "C" mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
   a.ntiles = (n + BQ - 1) / BQ;
   a.work = a.ntiles * kv->G * 8;
   a.scale_log2e = mi::kLog2e / sqrtf((float)D);
-  static bool attr_done = false;
   const size_t lds = LDS_HALVES * sizeof(_Float16);
-  if (!attr_done) {
-    MI_HIP(hipFuncSetAttribute((const void*)attn_prefill_kernel,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    attr_done = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};
+  MI_TRY(mi::set_lds_limit((const void*)attn_prefill_kernel, (int)lds, lds_set));
   const int grid = (a.work + 63) / 64 * 64;
   MI_HIP(mi::launch("attn_prefill", attn_prefill_kernel, dim3(grid), dim3(256), lds, s, a));
   return MI_OK;

@@ -135,9 +135,7 @@ extern "C" mi_status mi_qk_norm_rope_append(mi_kv* kv, int32_t layer, const floa
                                             int64_t pos, int32_t n, mi_f16* q_out,
                                             mi_f16* gate_out, mi_stream stream) {
   mi::clear_error();
-  if (!kv) return mi::fail(MI_ERR_INVALID_ARG, "null cache handle");
-  if (layer < 0 || layer >= kv->layers)
-    return mi::fail(MI_ERR_OUT_OF_RANGE, "layer=%d of %d", layer, kv->layers);
+  MI_TRY(mi::check_layer(kv, layer));
   if (!q_proj || !k || !v || !q_norm_w || !k_norm_w || !q_out || !gate_out)
     return mi::fail(MI_ERR_INVALID_ARG, "null pointer");
   if (n <= 0) return mi::fail(MI_ERR_INVALID_ARG, "n=%d", n);
