@@ -161,22 +161,27 @@ mi_status realloc_layers(mi_kv* kv, int64_t cap, int64_t keep_rows) {
   std::vector<_Float16*> nk(kv->layers, nullptr), nv(kv->layers, nullptr);
   size_t bytes = layer_bytes(kv, cap);
   size_t keep = layer_bytes(kv, keep_rows);
+  auto drop_new = [&](hipError_t e, const char* what) {
+    for (auto p : nk) if (p) (void)hipFree(p);
+    for (auto p : nv) if (p) (void)hipFree(p);
+    return mi::hip_status(e, what);
+  };
+  // Work already enqueued on any stream (appends into the old buffers
+  // included) completes before the rows are copied.
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return mi::hip_status(e, "hipDeviceSynchronize");
   for (int l = 0; l < kv->layers; l++) {
-    hipError_t e1 = hipMalloc((void**)&nk[l], bytes);
-    hipError_t e2 = (e1 == hipSuccess) ? hipMalloc((void**)&nv[l], bytes) : e1;
-    if (e2 != hipSuccess) {
-      for (auto p : nk) if (p) (void)hipFree(p);
-      for (auto p : nv) if (p) (void)hipFree(p);
-      return mi::hip_status(e2, "hipMalloc(kv cache)");
-    }
-    if (keep) {
-      MI_HIP(hipMemcpy(nk[l], kv->k[l], keep, hipMemcpyDeviceToDevice));
-      MI_HIP(hipMemcpy(nv[l], kv->v[l], keep, hipMemcpyDeviceToDevice));
-    }
-    MI_HIP(hipMemset((char*)nk[l] + keep, 0, bytes - keep));
-    MI_HIP(hipMemset((char*)nv[l] + keep, 0, bytes - keep));
+    if ((e = hipMalloc((void**)&nk[l], bytes)) != hipSuccess ||
+        (e = hipMalloc((void**)&nv[l], bytes)) != hipSuccess)
+      return drop_new(e, "hipMalloc(kv cache)");
+    if (keep && ((e = hipMemcpy(nk[l], kv->k[l], keep, hipMemcpyDeviceToDevice)) != hipSuccess ||
+                 (e = hipMemcpy(nv[l], kv->v[l], keep, hipMemcpyDeviceToDevice)) != hipSuccess))
+      return drop_new(e, "hipMemcpy(kv cache rows)");
+    if ((e = hipMemset((char*)nk[l] + keep, 0, bytes - keep)) != hipSuccess ||
+        (e = hipMemset((char*)nv[l] + keep, 0, bytes - keep)) != hipSuccess)
+      return drop_new(e, "hipMemset(kv cache)");
   }
-  MI_HIP(hipDeviceSynchronize());
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return drop_new(e, "hipDeviceSynchronize");
   free_layers(kv);
   kv->k = nk;
   kv->v = nv;

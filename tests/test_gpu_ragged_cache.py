@@ -243,3 +243,32 @@ def test_load_reference_float32_file(tmp_path):
         a, b = c.download(i, rows=rows), e.download(i, rows=rows)
         assert np.array_equal(a[0].view(np.uint16), b[0].view(np.uint16))
         assert np.array_equal(a[1].view(np.uint16), b[1].view(np.uint16))
+
+
+def test_growth_after_queued_appends_on_a_side_stream():
+    """Appends queued on a non-blocking stream, then a step past the capacity
+    (which regrows the cache) on the same stream without a host sync: the
+    regrow waits for the queued appends, so every row survives the copy."""
+    announce("growth after queued appends on a side stream")
+    rng = np.random.default_rng(17)
+    c = Cache(num_layers=1, capacity=256)
+    T = 260
+    ks, vs = f16(rng, T, G * D), f16(rng, T, G * D)
+    kd_all, vd_all = dev(ks), dev(vs)
+    q = dev(f16(rng, H * D))
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        for t in range(T):
+            out = attn_step_wrapper(c, q, kd_all[t], vd_all[t], t)
+    s.synchronize()
+    assert c.capacity >= T
+    kd, vd = c.download(0, rows=T)
+    assert np.array_equal(kd.view(np.uint16), ks.view(np.uint16))
+    assert np.array_equal(vd.view(np.uint16), vs.view(np.uint16))
+    assert_close(out, O.decode(host(q), ks, vs, T), "decode after growth on a side stream")
+
+
+def attn_step_wrapper(c, q, k, v, t):
+    from moe_infer_amd import attn_step
+    return attn_step(c, 0, q, k, v, t)
