@@ -192,6 +192,24 @@ def main():
                        backlog_ms=args.steps * LAYERS * 0.35 + 20)
         rope_us, _ = _lib.prof_read("qk_norm_rope")
         _lib.prof_enable(False)
+        # The same 10-layer step captured once as a HIP graph and replayed:
+        # the 20 launches leave the host path (arguments are fixed per capture,
+        # as in a serving loop that re-captures per position bucket).  The
+        # replay must reproduce the eager outputs bit for bit.
+        decode_step()
+        torch.cuda.synchronize()
+        eager = [o.clone() for o in outs]
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            decode_step()
+        graph.replay()
+        torch.cuda.synchronize()
+        graph_ok = all(torch.equal(a.view(torch.int16), b.view(torch.int16))
+                       for a, b in zip(eager, outs))
+        ms_graph = timed(graph.replay, args.steps, args.warmup,
+                         backlog_ms=args.steps * LAYERS * 0.25 + 20)
+        _lib.prof_enable(False)
+        del graph
         us_layer = ms * 1000 / LAYERS
         rec["decode"] = {
             "proj_step_us_per_layer": ms_proj * 1000 / LAYERS,
@@ -201,11 +219,14 @@ def main():
             "attend_only_us_per_layer": ms_attend * 1000 / LAYERS,
             "split_kernel_us": split_us, "combine_kernel_us": comb_us, "launches": n_split,
             "bytes_per_layer": C2_BYTES, "ms_per_step": ms,
+            "graph_step_us_per_layer": ms_graph * 1000 / LAYERS,
+            "graph_gbps": C2_BYTES / (ms_graph * 1e6 / LAYERS), "graph_matches_eager": graph_ok,
         }
         print(f"[bench] decode step {us_layer:.2f} us/layer (attend only "
               f"{ms_attend * 100:.2f}, from projections {ms_proj * 100:.2f}: split "
               f"{proj_split_us:.2f} combine {proj_comb_us:.2f}; two calls {ms_two * 100:.2f}, "
-              f"rope kernel {rope_us:.2f}) split {split_us:.2f} us combine {comb_us:.2f} us",
+              f"rope kernel {rope_us:.2f}) split {split_us:.2f} us combine {comb_us:.2f} us; "
+              f"graph replay {ms_graph * 100:.2f} us/layer (matches eager: {graph_ok})",
               file=sys.stderr, flush=True)
         del cache
 

@@ -9,7 +9,7 @@ from moe_infer_amd import Cache, attn_decode, attn_step, attn_verify
 from oracle import oracle as O
 
 from .conftest import f16
-from .gpu_util import announce, assert_close, dev
+from .gpu_util import announce, assert_close, dev, host
 
 pytestmark = pytest.mark.gpu
 H, G, D = 16, 2, 256
@@ -166,3 +166,50 @@ def test_step_sequence_long_context():
         if t % 50 == 0 or t == P + 199:
             assert_close(out, O.decode(q, np.concatenate(ks), np.concatenate(vs), t + 1, gate=g),
                          f"step t={t}")
+
+
+def test_graph_replay_of_steps_matches_eager():
+    """The engine step, the verify call and the step from projections
+    captured in one HIP graph (no allocation or memset inside the library
+    calls once the workspace exists); every replay, with eager work and host
+    synchronisations between replays, equals the eager outputs bit for bit."""
+    from moe_infer_amd import attn_step_proj
+    announce("graph replay of step / verify / step_proj")
+    rng = np.random.default_rng(31)
+    L = 5000
+    k, v = f16(rng, L + 8, G * D), f16(rng, L + 8, G * D)
+    c = filled_cache(k[:L], v[:L], capacity=L + 64)
+    q, g = dev(f16(rng, H * D)), dev(f16(rng, H * D))
+    kn, vn = dev(k[L]), dev(v[L])
+    q4, g4 = dev(f16(rng, 4, H, D)), dev(f16(rng, 4, H, D))
+    k4, v4 = dev(k[L + 1:L + 5]), dev(v[L + 1:L + 5])
+    qp = torch.from_numpy(rng.standard_normal((H, 2 * D)).astype(np.float32)).cuda()
+    kp = torch.from_numpy(rng.standard_normal((G, D)).astype(np.float32)).cuda()
+    vp = torch.from_numpy(rng.standard_normal((G, D)).astype(np.float32)).cuda()
+    qw = torch.ones(D, dtype=torch.bfloat16, device="cuda")
+    out1 = torch.empty(H * D, dtype=torch.float16, device="cuda")
+    out4 = torch.empty(4, H, D, dtype=torch.float16, device="cuda")
+    out3 = torch.empty(H, D, dtype=torch.float16, device="cuda")
+
+    def step():
+        attn_step(c, 0, q, kn, vn, L, gate=g, out=out1)
+        attn_verify(c, 0, q4, k4, v4, L + 1, gate=g4, out=out4)
+        attn_step_proj(c, 0, qp, kp, vp, qw, qw, L + 5, out=out3)
+
+    step()  # eager: sizes the workspace, sets the kernels' LDS limits
+    torch.cuda.synchronize()
+    ref = [out1.clone(), out4.clone(), out3.clone()]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    other = filled_cache(k[:300], v[:300])
+    for r in range(4):
+        for o in (out1, out4, out3):
+            o.fill_(7.0)
+        graph.replay()
+        attn_decode(other, 0, q, 300)  # eager work between the replays
+        torch.cuda.synchronize()
+        for a, b in zip(ref, (out1, out4, out3)):
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"replay {r}"
+    assert_close(out1, O.decode(host(q), k[:L + 1], v[:L + 1], L + 1, gate=host(g)),
+                 "graph step vs oracle")
