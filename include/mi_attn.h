@@ -282,7 +282,7 @@ mi_status mi_matvec_q4(const mi_f16* x, const uint32_t* w_packed,
  * kernel granularity).  mi_prof_enable synchronises the device and clears
  * earlier records.  Kernel names: "attn_split", "attn_combine",
  * "attn_prefill", "kv_pack",
- * "qk_norm_rope", "matvec_bf16", "matvec_q4".
+ * "qk_norm_rope", "matvec_bf16", "matvec_q4", "ragged_plan".
  * mi_prof_read returns the mean duration in microseconds and the number of
  * launches recorded since the last enable. */
 void mi_prof_enable(int on);

@@ -27,6 +27,7 @@
 //  * The waves of a workgroup merge their (m, l, O) through LDS and write one
 //    partial per chunk; attn_combine_kernel merges the chunks, normalises,
 //    applies the sigmoid gate and writes f16.
+#include <algorithm>
 #include <cstdlib>
 #include <type_traits>
 
@@ -45,10 +46,18 @@ struct SplitArgs {
   int64_t kv_len;           // non-ragged: rows the launch may read
   int64_t lim0;             // non-ragged: rows visible to query token 0
   const _Float16* q;        // [batch][nq][H][D]
-  float* part_o;            // [batch][G][max_chunks][ncols][D]
-  float* part_ml;           // [batch][G][max_chunks][ncols][2]
+  float* part_o;            // [G][nslots][ncols][D], slot = s * max_chunks + chunk
+  float* part_ml;           // [G][nslots][ncols][2]  (flat ragged: slot = workgroup + s)
+  int64_t nslots;
   int G, H, nq, chunk, max_chunks;
   float scale_log2e;
+  // Flat ragged split: tile_off[s] = 32-key tiles of sequences 0..s-1
+  // (invalid descriptors count 0), tile_off[batch] = all tiles T; workgroup
+  // x < nw = min(gridDim.x, T) takes tiles [x T / nw, (x+1) T / nw) of the
+  // concatenation and writes one partial per sequence it touches, in slot
+  // x + s.  Null otherwise.
+  const int32_t* tile_off;
+  int batch;
   // Optional fused append (decode step, verify): rows [app0, app0 + app_n)
   // of the cache are written from app_k / app_v ([app_n][G*D] token-major)
   // by the workgroup whose key chunk holds them, before it reads them.
@@ -198,7 +207,7 @@ struct HeadPart {
 // With X = ProjArgs (decode step from projections, one token, NCB = 1) the
 // kernel also norms and rotates Q per wave, and the workgroup holding row
 // app0 norms, rotates and appends K and appends V.
-template <int NWH, int NCB, int GH, typename X>
+template <int NWH, int NCB, int GH, typename X, bool FLAT>
 __global__ void __launch_bounds__(NWH * GH * 64)
 attn_split_kernel(SplitArgs a, X x) {
   constexpr bool kProj = is_proj<X>::value;
@@ -211,12 +220,30 @@ attn_split_kernel(SplitArgs a, X x) {
   const int j = lane & 15;   // column within a column block / A-operand row
   const int chunk_idx = blockIdx.x;
   const int kvh = blockIdx.y * GH + hw;
-  const int s = blockIdx.z;
+  int s = blockIdx.z;
   const int G = a.G;
   const int ncols = a.nq * 8;
 
-  int64_t len, row0, lim0;
-  if (a.lengths) {
+  constexpr bool flat = FLAT;  // the flat ragged split (a.tile_off)
+  int64_t len = 0, row0 = 0, lim0 = 0, key_begin = 0, key_end = 0;
+  int64_t t_lo = 0, t_hi = 0;  // flat: this workgroup's tiles of the concatenation
+  if constexpr (flat) {
+    // min(gridDim.x, T) workgroups take the tiles, each at least one
+    // (uniform values: kept in scalar registers)
+    const int64_t total = __builtin_amdgcn_readfirstlane(a.tile_off[a.batch]);
+    const int64_t nw = min((int64_t)gridDim.x, total);
+    if (chunk_idx >= nw) return;  // uniform
+    t_lo = (int64_t)chunk_idx * total / nw;
+    t_hi = (int64_t)(chunk_idx + 1) * total / nw;
+    // the sequence holding tile t_lo: the last s with tile_off[s] <= t_lo
+    int lo = 0, hi = a.batch - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (__builtin_amdgcn_readfirstlane(a.tile_off[mid]) <= t_lo) lo = mid;
+      else hi = mid - 1;
+    }
+    s = lo;
+  } else if (a.lengths) {
     len = a.lengths[s];
     row0 = a.offsets[s];
     lim0 = len;
@@ -227,9 +254,11 @@ attn_split_kernel(SplitArgs a, X x) {
     row0 = 0;
     lim0 = a.lim0;
   }
-  const int64_t key_begin = (int64_t)chunk_idx * a.chunk;
-  if (key_begin >= len) return;  // uniform over the workgroup
-  const int64_t key_end = min(key_begin + (int64_t)a.chunk, len);
+  if constexpr (!flat) {
+    key_begin = (int64_t)chunk_idx * a.chunk;
+    if (key_begin >= len) return;  // uniform over the workgroup
+    key_end = min(key_begin + (int64_t)a.chunk, len);
+  }
 
   // K operand rows: tile u, A-row j <-> key k0 + 8*(j/4) + 4u + j%4, so that
   // accumulator row 4g+e of tile u is key k0 + 8g + 4u + e.  In the 32-row
@@ -272,7 +301,7 @@ attn_split_kernel(SplitArgs a, X x) {
   HeadPart<kProj ? D / kTPH : 4> qpart;
   f16x8 kf[2][8], vf[16];
   bool peeled = false;
-  const int64_t kfirst = key_begin + 32 * w;
+  int64_t kfirst = key_begin + 32 * w;
   if constexpr (kProj) {
     qpart.load(x.q_proj + ((int64_t)blockIdx.y * GH * 8 + threadIdx.x / kTPH) * (2 * D), x.q_w,
                lane);
@@ -337,6 +366,21 @@ attn_split_kernel(SplitArgs a, X x) {
     }
   }
 
+
+  // One pass per key range: once, or per sequence segment of a flat range.
+  for (;;) {
+  int64_t pslot = (int64_t)s * a.max_chunks + chunk_idx;  // partial slot
+  if constexpr (flat) {
+    const int64_t ps = __builtin_amdgcn_readfirstlane(a.tile_off[s]);
+    const int64_t pe = __builtin_amdgcn_readfirstlane(a.tile_off[s + 1]);
+    len = __builtin_amdgcn_readfirstlane(a.lengths[s]);
+    row0 = __builtin_amdgcn_readfirstlane(a.offsets[s]);
+    lim0 = len;
+    key_begin = 32 * (max(t_lo, ps) - ps);
+    key_end = min(32 * (min(t_hi, pe) - ps), len);
+    kfirst = key_begin + 32 * w;
+    pslot = (int64_t)chunk_idx + s;
+  }
 
   // Q^T operand: lane (g, j) holds q[token][head][32kk + 8g + 0..7] for its
   // column j, kk = 0..7 (the column chunk 4kk + g the K operand of the same
@@ -499,8 +543,7 @@ attn_split_kernel(SplitArgs a, X x) {
       sw2[ww * ncols + c] = sc;
       L += sl2[ww * ncols + c] * sc;
     }
-    const int64_t pb =
-        (((int64_t)s * G + blockIdx.y * GH + h2) * a.max_chunks + chunk_idx) * ncols + c;
+    const int64_t pb = ((int64_t)(blockIdx.y * GH + h2) * a.nslots + pslot) * ncols + c;
     store_part(M, a.part_ml + pb * 2 + 0);
     store_part(L, a.part_ml + pb * 2 + 1);
   }
@@ -516,9 +559,16 @@ attn_split_kernel(SplitArgs a, X x) {
 #pragma unroll
     for (int ww = 0; ww < NWH; ww++)
       o += *(const f32x4*)(so2 + (ww * ncols + c) * kLdsRow + d4) * sw2[ww * ncols + c];
-    const int64_t pb =
-        (((int64_t)s * G + blockIdx.y * GH + h2) * a.max_chunks + chunk_idx) * ncols + c;
+    const int64_t pb = ((int64_t)(blockIdx.y * GH + h2) * a.nslots + pslot) * ncols + c;
     store_part(o, (f32x4*)(a.part_o + pb * D + d4));
+  }
+  if constexpr (!flat) break;
+  if (__builtin_amdgcn_readfirstlane(a.tile_off[s + 1]) >= t_hi) break;
+  // next sequence with tiles (the range ends inside a later one)
+  do s++;
+  while (__builtin_amdgcn_readfirstlane(a.tile_off[s + 1]) ==
+         __builtin_amdgcn_readfirstlane(a.tile_off[s]));
+  __syncthreads();  // the LDS merge area is reused
   }
 }
 
@@ -532,6 +582,9 @@ struct CombineArgs {
   const float* gate32;     // or the gate halves of q_proj [nq][H][2*D] (else null)
   _Float16* out;           // [batch][nq][H][D]
   int G, H, nq, chunk, max_chunks;
+  const int32_t* tile_off;  // flat ragged split (SplitArgs::tile_off), else null
+  int nwg, batch;           // flat: the split launch's gridDim.x; sequences
+  int64_t nslots;           // partial slots per KV head (SplitArgs::nslots)
 };
 
 // Chunk merge.  One workgroup per (column, KV head x 16-column slice,
@@ -570,11 +623,11 @@ attn_combine_kernel(CombineArgs a) {
     if (bad) len = 0;
   }
   const int nch = (int)((len + a.chunk - 1) / a.chunk);
-  const int64_t pbase = ((int64_t)s * a.G + kvh) * a.max_chunks;
-  const float* ml = a.part_ml + (pbase * ncols + c) * 2;  // chunk ch at ml[ch * mstride]
+  const int64_t base = (int64_t)s * a.max_chunks;  // first partial slot of s
+  const float* ml = a.part_ml + ((kvh * a.nslots + base) * ncols + c) * 2;  // chunk ch at ml[ch * mstride]
   const int64_t mstride = (int64_t)ncols * 2;
   const int dl = t % kCombineSlice, cg = t / kCombineSlice;
-  const float* po = a.part_o + (pbase * ncols + c) * D + d0 + dl;
+  const float* po = a.part_o + ((kvh * a.nslots + base) * ncols + c) * D + d0 + dl;
   const int64_t ostride = (int64_t)ncols * D;
 
   float mloc[kMaxChunks / 256], lloc[kMaxChunks / 256];
@@ -642,6 +695,94 @@ attn_combine_kernel(CombineArgs a) {
   }
 }
 
+// Merge for the flat ragged split: a sequence has few partials (its tiles
+// span a few workgroups), so one workgroup per (column, KV head, sequence)
+// with one thread per d runs a single online-softmax pass over them.
+// Workgroup x < nw = min(nwg, T) of the split took tiles [x T / nw,
+// (x+1) T / nw), so tile t is in workgroup ceil((t+1) nw / T) - 1 and the
+// partials of sequence s are in slots first + s .. last + s.
+__global__ void __launch_bounds__(D)
+attn_combine_flat_kernel(CombineArgs a) {
+  const int c = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z, d = threadIdx.x;
+  const int ncols = a.nq * 8;
+  const int32_t len = a.lengths[s], off = a.offsets[s];
+  const bool bad = len < 0 || len > a.kv_len || off < 0 || (off & 31);
+  const int64_t total = a.tile_off[a.batch];
+  const int64_t ps = a.tile_off[s], pe = a.tile_off[s + 1];
+  int64_t first = 0, nch = 0;
+  if (pe > ps) {
+    const int64_t nw = min((int64_t)a.nwg, total);
+    first = ((ps + 1) * nw + total - 1) / total - 1;
+    nch = (pe * nw + total - 1) / total - 1 - first + 1;
+  }
+  const int64_t slot0 = (kvh * a.nslots + first + s) * ncols + c;
+  const float* ml = a.part_ml + slot0 * 2;
+  const float* po = a.part_o + slot0 * D + d;
+  float M = kNegBig, L = 0.f, o = 0.f;
+  constexpr int kB = 8;  // partials loaded per batch, all before their use
+  for (int64_t c0 = 0; c0 < nch; c0 += kB) {
+    float mb[kB], lb[kB], ob[kB];
+#pragma unroll
+    for (int k = 0; k < kB; k++) {
+      const bool in = c0 + k < nch;
+      mb[k] = in ? ml[(c0 + k) * ncols * 2] : kNegBig;
+      lb[k] = in ? ml[(c0 + k) * ncols * 2 + 1] : 0.f;
+      ob[k] = in ? po[(c0 + k) * ncols * D] : 0.f;
+    }
+    float mx = M;
+#pragma unroll
+    for (int k = 0; k < kB; k++) mx = fmaxf(mx, mb[k]);
+    const float sc = exp2f(M - mx);  // rescale what has been summed
+    L *= sc;
+    o *= sc;
+    M = mx;
+#pragma unroll
+    for (int k = 0; k < kB; k++) {
+      const float wgt = exp2f(mb[k] - M);
+      L += lb[k] * wgt;
+      o += ob[k] * wgt;
+    }
+  }
+  float r = (L > 0.f) ? o / L : 0.f;
+  if (bad) r = __builtin_nanf("");
+  const int hq = kvh * 8 + c;
+  const int64_t oidx = ((int64_t)s * a.H + hq) * D + d;
+  if (a.gate) r *= 1.f / (1.f + expf(-(float)a.gate[oidx]));
+  a.out[oidx] = (_Float16)r;
+}
+
+// Tile offsets of a ragged batch for the flat split: tile_off[s] = sum over
+// r < s of ceil(len_r / 32) (0 for an invalid descriptor), tile_off[batch] =
+// the total.  One workgroup, an exclusive scan per 256 sequences.
+__global__ void __launch_bounds__(256)
+ragged_plan_kernel(const int32_t* lengths, const int32_t* offsets, int batch, int64_t max_len,
+                   int32_t* tile_off) {
+  __shared__ int32_t scan[256];
+  const int t = threadIdx.x;
+  int32_t carry = 0;
+  for (int b0 = 0; b0 < batch; b0 += 256) {
+    const int sq = b0 + t;
+    int32_t n = 0;
+    if (sq < batch) {
+      const int32_t len = lengths[sq], off = offsets[sq];
+      const bool bad = len < 0 || len > max_len || off < 0 || (off & 31);
+      n = bad ? 0 : (len + 31) >> 5;
+    }
+    scan[t] = n;
+    __syncthreads();
+    for (int d = 1; d < 256; d <<= 1) {  // inclusive scan
+      const int32_t v = t >= d ? scan[t - d] : 0;
+      __syncthreads();
+      scan[t] += v;
+      __syncthreads();
+    }
+    if (sq < batch) tile_off[sq] = carry + scan[t] - n;
+    carry += scan[255];
+    __syncthreads();
+  }
+  if (t == 0) tile_off[batch] = carry;
+}
+
 int env_int(const char* name, int dflt) {
   const char* e = getenv(name);
   return (e && *e) ? atoi(e) : dflt;
@@ -687,15 +828,15 @@ SplitPlan plan_split(int64_t max_len, int64_t batch, int G, int nq) {
   return p;
 }
 
-template <int NWH, int NCB, int GH, typename X = NoProj>
+template <int NWH, int NCB, int GH, typename X = NoProj, bool FLAT = false>
 mi_status launch_split(const SplitArgs& a, int64_t batch, hipStream_t stream, const X& x = X()) {
   const int ncols = a.nq * 8;
   size_t lds = (size_t)GH * (NWH * ncols * (D + 4) + 3 * NWH * ncols + ncols) * sizeof(float);
   if constexpr (is_proj<X>::value) lds += (size_t)GH * 8 * (D + 8) * sizeof(_Float16);
   static std::atomic<uint64_t> lds_set{0};
-  MI_TRY(mi::set_lds_limit((const void*)attn_split_kernel<NWH, NCB, GH, X>, 160 * 1024, lds_set));
+  MI_TRY(mi::set_lds_limit((const void*)attn_split_kernel<NWH, NCB, GH, X, FLAT>, 160 * 1024, lds_set));
   dim3 grid(a.max_chunks, a.G / GH, (unsigned)batch);
-  MI_HIP(mi::launch("attn_split", attn_split_kernel<NWH, NCB, GH, X>, grid,
+  MI_HIP(mi::launch("attn_split", attn_split_kernel<NWH, NCB, GH, X, FLAT>, grid,
                     dim3(NWH * GH * 64), lds, stream, a, x));
   return MI_OK;
 }
@@ -712,6 +853,13 @@ mi_status launch_proj(const SplitArgs& a, const SplitPlan& plan, hipStream_t str
 size_t split_workspace_bytes(int64_t batch, int G, int max_chunks, int nq) {
   size_t units = (size_t)batch * G * max_chunks * nq * 8;
   return units * (D + 2) * sizeof(float) + 256;
+}
+
+// Flat ragged split: workgroups per KV-head group (one per CU), and the
+// workspace: partials of nwg + batch slots, then the tile offsets.
+int ragged_nwg(int G, int gh) { return std::max(1, 256 / std::max(1, G / gh)); }
+size_t ragged_workspace_bytes(int64_t batch, int G, int nwg) {
+  return split_workspace_bytes(1, G, nwg + (int)batch, 1) + (size_t)(batch + 1) * sizeof(int32_t);
 }
 
 // Runs split + combine for nq <= 4 query tokens per sequence.
@@ -749,11 +897,29 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
   a.vw = const_cast<_Float16*>(v);
   a.app0 = app.row0;
   a.app_n = app.n;
-  const size_t need = split_workspace_bytes(batch, G, a.max_chunks, nq);
+  a.tile_off = nullptr;
+  a.batch = (int)batch;
+  const int nwg = ragged_nwg(G, plan.gh);
+  const size_t need = lengths ? ragged_workspace_bytes(batch, G, nwg)
+                              : split_workspace_bytes(batch, G, a.max_chunks, nq);
   if (ws_bytes < need)
     return mi::fail(MI_ERR_INVALID_ARG, "workspace %zu bytes < %zu needed", ws_bytes, need);
+  const size_t slots = lengths ? (size_t)nwg + batch : (size_t)batch * a.max_chunks;
   a.part_o = (float*)ws;
-  a.part_ml = a.part_o + (size_t)batch * G * a.max_chunks * nq * 8 * D;
+  a.part_ml = a.part_o + slots * G * nq * 8 * D;
+  a.nslots = (int64_t)slots;
+  if (lengths) {
+    // flat split over the concatenated sequences (one nq = 1 token each)
+    if (nq != 1) return mi::fail(MI_ERR_INVALID_ARG, "ragged batches take one query token");
+    if ((int64_t)batch * ((max_len + 31) / 32) >= ((int64_t)1 << 31))
+      return mi::fail(MI_ERR_UNSUPPORTED, "batch * max_len / 32 beyond 2^31 tiles");
+    int32_t* tile_off = (int32_t*)(a.part_ml + slots * G * nq * 8 * 2);
+    MI_HIP(mi::launch("ragged_plan", ragged_plan_kernel, dim3(1), dim3(256), 0, stream, lengths,
+                      offsets, (int)batch, kv_len, tile_off));
+    a.tile_off = tile_off;
+    a.max_chunks = nwg;
+    a.chunk = 0;
+  }
   mi_status st;
   if (proj) {
     if (nq != 1 || batch != 1) return mi::fail(MI_ERR_INVALID_ARG, "projection input: one token");
@@ -765,6 +931,9 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
       case 4: st = launch_proj<4>(a, plan, stream, *proj); break;
       default: return mi::fail(MI_ERR_UNSUPPORTED, "rot_half=%d", proj->rot_half);
     }
+  } else if (lengths) {
+    st = plan.gh == 2 ? launch_split<4, 1, 2, NoProj, true>(a, 1, stream)
+                      : launch_split<8, 1, 1, NoProj, true>(a, 1, stream);
   } else if (plan.ncb == 2)
     st = launch_split<4, 2, 1>(a, batch, stream);
   else if (plan.gh == 2)
@@ -786,6 +955,15 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
   c.nq = nq;
   c.chunk = a.chunk;
   c.max_chunks = a.max_chunks;
+  c.tile_off = a.tile_off;
+  c.nslots = a.nslots;
+  c.nwg = nwg;
+  c.batch = (int)batch;
+  if (lengths) {
+    MI_HIP(mi::launch("attn_combine", attn_combine_flat_kernel, dim3(8, G, (unsigned)batch),
+                      dim3(D), 0, stream, c));
+    return MI_OK;
+  }
   dim3 grid(nq * 8, G * (D / kCombineSlice), (unsigned)batch);
   MI_HIP(mi::launch("attn_combine", attn_combine_kernel, grid, dim3(256), 0, stream, c));
   return MI_OK;
@@ -886,7 +1064,7 @@ extern "C" size_t mi_attn_ragged_workspace_size(int32_t batch, int32_t max_len,
   (void)num_q_heads;
   (void)head_dim;
   const SplitPlan plan = plan_split(max_len, batch, num_kv_heads, 1);
-  return split_workspace_bytes(batch, num_kv_heads, plan.max_chunks, 1);
+  return ragged_workspace_bytes(batch, num_kv_heads, ragged_nwg(num_kv_heads, plan.gh));
 }
 
 extern "C" mi_status mi_attn_decode_ragged(const mi_f16* k_rows, const mi_f16* v_rows,

@@ -28,7 +28,8 @@ def ragged_buffers(rng, lengths):
 
 
 @pytest.mark.parametrize("lengths", [[5, 0, 17, 1, 8, 9, 33, 300],
-                                     [1024, 1, 2049, 255, 4096, 0, 777, 129]])
+                                     [1024, 1, 2049, 255, 4096, 0, 777, 129],
+                                     [60000, 3]])  # one sequence over every workgroup
 def test_ragged_matches_oracle(lengths):
     announce(f"ragged {lengths}")
     rng = np.random.default_rng(sum(lengths))
@@ -79,6 +80,52 @@ def test_ragged_rejects_bad_tables():
         with pytest.raises(ValueError):
             attn_decode_ragged(kb, vb, torch.tensor(off, dtype=torch.int32).cuda(),
                                torch.tensor(ln, dtype=torch.int32).cuda(), q, 64)
+
+
+def test_ragged_many_sequences_flat_split():
+    """600 sequences (the tile-offset scan runs over three 256-sequence
+    blocks), lengths 0..300 with exact multiples of 32 among them: every
+    output equals the oracle, zero-length sequences are zero."""
+    announce("ragged 600 seqs")
+    rng = np.random.default_rng(600)
+    lengths = rng.integers(0, 301, size=600).astype(np.int32)
+    lengths[::7] = 0
+    lengths[3::11] = 64
+    lengths[5::13] = 32
+    offsets, k, v = ragged_buffers(rng, lengths)
+    b = len(lengths)
+    q, g = f16(rng, b, H, D), f16(rng, b, H, D)
+    kb, vb = kv_pack(dev(k), dev(v), G)
+    out = attn_decode_ragged(kb, vb, torch.from_numpy(offsets).cuda(),
+                             torch.from_numpy(lengths).cuda(), dev(q), int(lengths.max()),
+                             gate=dev(g))
+    ref = O.decode_ragged(q, k, v, offsets, lengths, gate=g)
+    assert_close(out, ref, "ragged 600 seqs")
+    assert np.all(host(out)[lengths == 0] == 0)
+
+
+def test_ragged_invalid_rows_report_nan_on_device():
+    """With host validation off, sequences whose descriptor is invalid
+    (unaligned offset, length past max_len, negative length) come out NaN;
+    the others are unaffected."""
+    announce("ragged invalid descriptors (device)")
+    rng = np.random.default_rng(9)
+    lengths = np.array([40, 50, 60, 70, 80], np.int32)
+    offsets, k, v = ragged_buffers(rng, lengths)
+    q = f16(rng, 5, H, D)
+    kb, vb = kv_pack(dev(k), dev(v), G)
+    bad_off = offsets.copy()
+    bad_len = lengths.copy()
+    bad_off[1] += 8         # not on a 32-row block
+    bad_len[3] = 1000       # past max_len
+    bad_len[4] = -2
+    out = host(attn_decode_ragged(kb, vb, torch.from_numpy(bad_off).cuda(),
+                                  torch.from_numpy(bad_len).cuda(), dev(q), 100,
+                                  validate=False))
+    assert np.all(np.isnan(out[[1, 3, 4]]))
+    for s in (0, 2):
+        a, n = offsets[s], lengths[s]
+        assert_close(out[s], O.decode(q[s], k[a:a + n], v[a:a + n], n), f"valid seq {s}")
 
 
 def test_pack_layout():
