@@ -293,24 +293,19 @@ attn_split_kernel(SplitArgs a, X x) {
   const int per_head = NWH * ncols * kLdsRow + 3 * NWH * ncols + ncols;
   _Float16* qs = (_Float16*)(smem + GH * per_head);  // [GH*8][kQRow]
   // Projection prologue, issue side: this lane's part of the q_proj rows
-  // (one query head per kTPH lanes of the workgroup) is loaded first, then
-  // the first tile's K and V, so the HBM stream starts at once.  The
-  // workgroup that appends row app0 reads its tiles after the append.
+  // (one query head per kTPH lanes of the workgroup).  The first K/V tile is
+  // loaded in the tile loop, after the prologue: issuing it here keeps 128
+  // registers live through the norm and rotation, which spills (measured
+  // 2 us slower per step).
   constexpr int kTPH = NWH * 8;
   RopeTab<X::kSH> tab;
   HeadPart<kProj ? D / kTPH : 4> qpart;
   f16x8 kf[2][8], vf[16];
-  bool peeled = false;
   int64_t kfirst = key_begin + 32 * w;
   if constexpr (kProj) {
     qpart.load(x.q_proj + ((int64_t)blockIdx.y * GH * 8 + threadIdx.x / kTPH) * (2 * D), x.q_w,
                lane);
     tab.fill(x, lane);
-    peeled = !(key_begin <= a.app0 && a.app0 < key_end) && kfirst < key_end;
-    if (peeled) {
-      load_k(kfirst, kf);
-      load_v(kfirst, vf);
-    }
   }
 
   if constexpr (kProj) {
@@ -445,10 +440,8 @@ attn_split_kernel(SplitArgs a, X x) {
   }
 
   for (int64_t k0 = kfirst; k0 < key_end; k0 += 32 * NWH) {
-    if (!peeled || k0 != kfirst) {
-      load_k(k0, kf);
-      load_v(k0, vf);
-    }
+    load_k(k0, kf);
+    load_v(k0, vf);
     if (k0 + 32 > key_end) {  // the last, partial tile (wave-uniform branch)
       const int64_t valid = key_end - (k0 + 8 * g);
 #pragma unroll
