@@ -36,6 +36,10 @@ constexpr int K_TILE_HALVES = 2 * KSUB;
 constexpr int V_TILE_HALVES = BK * D;  // 8 blocks of [D][8]
 // LDS: K tiles double-buffered at [0, 2*K_TILE_HALVES), V tiles after them.
 constexpr int LDS_HALVES = 2 * (K_TILE_HALVES + V_TILE_HALVES);
+// Epilogue staging of O (f32, one padded row of D per query of the 4 waves),
+// over the tile buffers once every wave has finished its last tile.
+constexpr int O_ROW = D + 4;
+constexpr int LDS_BYTES = LDS_HALVES * 2 > 4 * 32 * O_ROW * 4 ? LDS_HALVES * 2 : 4 * 32 * O_ROW * 4;
 constexpr float kNegBig = -1e30f;
 
 struct PrefillArgs {
@@ -335,24 +339,47 @@ attn_prefill_kernel(PrefillArgs a) {
   }
   if (pending) pv(nt - 1, pprev);
 
-  if (qi >= a.n) return;
+  // Epilogue: O / l goes to LDS as f32 rows (query-major), then every query
+  // row of D outputs is written by 32 lanes with 16-byte stores (two rows per
+  // wave instruction), the gate read the same way; the accumulator layout
+  // would otherwise make each lane store 8 bytes into 32 rows 8 KiB apart.
+  __syncthreads();  // every wave is done with the K/V tiles
+  float* ob = (float*)lds + w * 32 * O_ROW;
   const float inv = (l > 0.f) ? 1.f / l : 0.f;
-  const int64_t obase = ((int64_t)qi * a.H + hq) * D;
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
+  for (int i = 0; i < 8; i++)
 #pragma unroll
     for (int e4 = 0; e4 < 4; e4++) {
-      const int d = i * 32 + 8 * e4 + 4 * hl;
-      f16x4 o;
-      f16x4 gv = a.gate ? *(const f16x4*)(a.gate + obase + d) : f16x4{};
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; e++) o[e] = acc[i][4 * e4 + e] * inv;
+      *(f32x4*)(ob + col * O_ROW + i * 32 + 8 * e4 + 4 * hl) = o;
+    }
+  mi::sync_lds();
+  const int dc = 8 * (lane & 31);  // this lane's 8 columns of a row
+#pragma unroll 4
+  for (int st = 0; st < 16; st++) {
+    const int r = 2 * st + hl;  // query row of the wave
+    const int qr = q0 + 32 * w + r;
+    if (qr >= a.n) continue;
+    const float* src = ob + r * O_ROW + dc;
+    const f32x4 x0 = *(const f32x4*)src, x1 = *(const f32x4*)(src + 4);
+    const int64_t obase = ((int64_t)qr * a.H + hq) * D + dc;
+    f16x8 y;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      y[e] = (_Float16)x0[e];
+      y[4 + e] = (_Float16)x1[e];
+    }
+    if (a.gate) {
+      const f16x8 gv = *(const f16x8*)(a.gate + obase);
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        float x = acc[i][4 * e4 + e] * inv;
-        if (a.gate) x *= 1.f / (1.f + expf(-(float)gv[e]));
-        o[e] = (_Float16)x;
+        y[e] = (_Float16)(x0[e] / (1.f + expf(-(float)gv[e])));
+        y[4 + e] = (_Float16)(x1[e] / (1.f + expf(-(float)gv[4 + e])));
       }
-      *(f16x4*)(a.out + obase + d) = o;
     }
+    *(f16x8*)(a.out + obase) = y;
   }
 }
 
@@ -396,7 +423,7 @@ extern "C" mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
   a.ntiles = (n + BQ - 1) / BQ;
   a.work = a.ntiles * kv->G * 8;
   a.scale_log2e = mi::kLog2e / sqrtf((float)D);
-  const size_t lds = LDS_HALVES * sizeof(_Float16);
+  const size_t lds = LDS_BYTES;
   static std::atomic<uint64_t> lds_set{0};
   MI_TRY(mi::set_lds_limit((const void*)attn_prefill_kernel, (int)lds, lds_set));
   const int grid = (a.work + 63) / 64 * 64;
