@@ -1073,6 +1073,8 @@ extern "C" mi_status mi_attn_decode_ragged(const mi_f16* k_rows, const mi_f16* v
     return mi::fail(MI_ERR_INVALID_ARG, "null pointer argument");
   if (batch <= 0 || max_len < 0)
     return mi::fail(MI_ERR_INVALID_ARG, "batch=%d max_len=%d", batch, max_len);
+  if (batch > 65535)  // the merge launch has one grid row per sequence
+    return mi::fail(MI_ERR_UNSUPPORTED, "batch=%d above 65535 sequences", batch);
   const int64_t ml = max_len > 0 ? max_len : 1;
   return run_split((const _Float16*)k_rows, (const _Float16*)v_rows, offsets, lengths, ml, 0,
                    ml, batch, num_q_heads, num_kv_heads, 1, (const _Float16*)q,

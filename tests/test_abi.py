@@ -55,5 +55,9 @@ def test_host_side_errors_without_gpu():
                                      None, 0, None) == _lib.MI_ERR_INVALID_ARG
     assert lib.mi_attn_decode_ragged(None, None, None, None, 1, 1, 16, 2, 64, None, None, None,
                                      None, 0, None) == _lib.MI_ERR_UNSUPPORTED
+    fake = C.c_void_p(256)  # never dereferenced: the argument checks come first
+    assert lib.mi_attn_decode_ragged(fake, fake, fake, fake, 70000, 1, 16, 2, 256, fake, None,
+                                     fake, fake, 1 << 20, None) == _lib.MI_ERR_UNSUPPORTED
+    assert b"65535" in lib.mi_last_error()
     with pytest.raises(_lib.MiValueError):
         _lib.check(lib.mi_kv_set_pos(None, 0))
