@@ -290,7 +290,7 @@ attn_split_kernel(SplitArgs a, X x) {
   // workgroup's GH*8 heads.
   constexpr int kLdsRow = D + 4;
   constexpr int kQRow = D + 8;
-  const int per_head = NWH * ncols * kLdsRow + 3 * NWH * ncols + ncols;
+  const int per_head = NWH * ncols * kLdsRow + 2 * NWH * ncols;
   _Float16* qs = (_Float16*)(smem + GH * per_head);  // [GH*8][kQRow]
   // Projection prologue, issue side: this lane's part of the q_proj rows
   // (one query head per kTPH lanes of the workgroup).  The first K/V tile is
@@ -501,8 +501,7 @@ attn_split_kernel(SplitArgs a, X x) {
 
   // ---- merge the NWH waves of each head through LDS.  Per head:
   // O [NWH][ncols][kLdsRow] (row padded by 4 floats so the 16 columns a
-  // lane group writes fall in distinct banks), then m, l [NWH][ncols], then
-  // the merge weights 2^(m_w - M) [NWH][ncols] and the merged l [ncols].
+  // lane group writes fall in distinct banks), then m, l [NWH][ncols].
   float* so = smem + hw * per_head;
   float* sm = so + NWH * ncols * kLdsRow;
   float* sl = sm + NWH * ncols;
@@ -520,39 +519,33 @@ attn_split_kernel(SplitArgs a, X x) {
     }
   }
   __syncthreads();
-  // weights: one thread per (head, column)
-  if ((int)threadIdx.x < GH * ncols) {
-    const int h2 = threadIdx.x / ncols, c = threadIdx.x % ncols;
-    float* sm2 = smem + h2 * per_head + NWH * ncols * kLdsRow;
-    float* sl2 = sm2 + NWH * ncols;
-    float* sw2 = sl2 + NWH * ncols;
-    float M = kNegBig;
-#pragma unroll
-    for (int ww = 0; ww < NWH; ww++) M = fmaxf(M, sm2[ww * ncols + c]);
-    float L = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < NWH; ww++) {
-      const float sc = exp2f(sm2[ww * ncols + c] - M);
-      sw2[ww * ncols + c] = sc;
-      L += sl2[ww * ncols + c] * sc;
-    }
-    const int64_t pb = ((int64_t)(blockIdx.y * GH + h2) * a.nslots + pslot) * ncols + c;
-    store_part(M, a.part_ml + pb * 2 + 0);
-    store_part(L, a.part_ml + pb * 2 + 1);
-  }
-  __syncthreads();
-  // merged O, four columns of d per thread
+  // merged O, four columns of d per thread; each thread derives its column's
+  // merge weights 2^(m_w - M) from the NWH waves' (m, l) itself (four
+  // exponentials), which saves a barrier on the kernel's critical path; the
+  // threads of d4 = 0 also store the merged (M, L).
   for (int idx = threadIdx.x; idx < GH * ncols * (D / 4); idx += NWH * GH * 64) {
     const int h2 = idx / (ncols * (D / 4));
     const int c = (idx / (D / 4)) % ncols;
     const int d4 = (idx % (D / 4)) * 4;
     const float* so2 = smem + h2 * per_head;
-    const float* sw2 = so2 + NWH * ncols * kLdsRow + 2 * NWH * ncols;
+    const float* sm2 = so2 + NWH * ncols * kLdsRow;
+    const float* sl2 = sm2 + NWH * ncols;
+    float M = kNegBig;
+#pragma unroll
+    for (int ww = 0; ww < NWH; ww++) M = fmaxf(M, sm2[ww * ncols + c]);
+    float L = 0.f;
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ww = 0; ww < NWH; ww++)
-      o += *(const f32x4*)(so2 + (ww * ncols + c) * kLdsRow + d4) * sw2[ww * ncols + c];
+    for (int ww = 0; ww < NWH; ww++) {
+      const float sc = exp2f(sm2[ww * ncols + c] - M);
+      L += sl2[ww * ncols + c] * sc;
+      o += *(const f32x4*)(so2 + (ww * ncols + c) * kLdsRow + d4) * sc;
+    }
     const int64_t pb = ((int64_t)(blockIdx.y * GH + h2) * a.nslots + pslot) * ncols + c;
+    if (d4 == 0) {
+      store_part(M, a.part_ml + pb * 2 + 0);
+      store_part(L, a.part_ml + pb * 2 + 1);
+    }
     store_part(o, (f32x4*)(a.part_o + pb * D + d4));
   }
   if constexpr (!flat) break;
@@ -824,7 +817,7 @@ SplitPlan plan_split(int64_t max_len, int64_t batch, int G, int nq) {
 template <int NWH, int NCB, int GH, typename X = NoProj, bool FLAT = false>
 mi_status launch_split(const SplitArgs& a, int64_t batch, hipStream_t stream, const X& x = X()) {
   const int ncols = a.nq * 8;
-  size_t lds = (size_t)GH * (NWH * ncols * (D + 4) + 3 * NWH * ncols + ncols) * sizeof(float);
+  size_t lds = (size_t)GH * (NWH * ncols * (D + 4) + 2 * NWH * ncols) * sizeof(float);
   if constexpr (is_proj<X>::value) lds += (size_t)GH * 8 * (D + 8) * sizeof(_Float16);
   static std::atomic<uint64_t> lds_set{0};
   MI_TRY(mi::set_lds_limit((const void*)attn_split_kernel<NWH, NCB, GH, X, FLAT>, 160 * 1024, lds_set));
