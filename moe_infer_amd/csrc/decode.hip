@@ -774,6 +774,20 @@ int env_int(const char* name, int dflt) {
   return (e && *e) ? atoi(e) : dflt;
 }
 
+// Split-planning knobs, read once per process (measurement aids; the
+// defaults are the tuned values): MI_ATTN_SPLIT_GH=1 puts one KV head per
+// workgroup, MI_ATTN_SPLIT_WGS sets the target workgroup count,
+// MI_ATTN_SPLIT_CHUNK fixes the keys per chunk.
+struct SplitKnobs {
+  int gh, wgs, chunk;
+};
+const SplitKnobs& split_knobs() {
+  static const SplitKnobs k{env_int("MI_ATTN_SPLIT_GH", 2),
+                            std::max(1, env_int("MI_ATTN_SPLIT_WGS", 256)),
+                            std::max(0, env_int("MI_ATTN_SPLIT_CHUNK", 0))};
+  return k;
+}
+
 struct SplitPlan {
   int nwh, gh, ncb, chunk, max_chunks;
 };
@@ -790,7 +804,7 @@ SplitPlan plan_split(int64_t max_len, int64_t batch, int G, int nq) {
   if (p.ncb == 2) {  // 32 columns: 4 waves, one head (registers and LDS)
     p.nwh = 4;
     p.gh = 1;
-  } else if (G % 2 == 0 && env_int("MI_ATTN_SPLIT_GH", 2) == 2) {
+  } else if (G % 2 == 0 && split_knobs().gh == 2) {
     p.nwh = 4;
     p.gh = 2;
   } else {
@@ -798,8 +812,8 @@ SplitPlan plan_split(int64_t max_len, int64_t batch, int G, int nq) {
     p.gh = 1;
   }
   const int64_t step = 32 * p.nwh;
-  const int64_t target_wgs = env_int("MI_ATTN_SPLIT_WGS", 256);
-  int64_t chunk = env_int("MI_ATTN_SPLIT_CHUNK", 0);
+  const int64_t target_wgs = split_knobs().wgs;
+  int64_t chunk = split_knobs().chunk;
   if (chunk <= 0) {
     chunk = (batch * G * max_len + p.gh * target_wgs - 1) / (p.gh * target_wgs);
     if (chunk > 2048) chunk = 2048;
