@@ -48,6 +48,19 @@ def test_decode_ctx32k_matches_oracle():
     assert_close(out, O.decode_f64(q, k, v, L), "decode L=32768 vs f64 oracle")
 
 
+def test_decode_quarter_million_rows():
+    """262161 rows (chunks of 1152 keys, 228 per head): the long-context
+    chunking against the oracle."""
+    announce("decode L=262161")
+    L = 262161
+    rng = np.random.default_rng(262)
+    q, g = f16(rng, H * D), f16(rng, H * D)
+    k, v = f16(rng, L, G * D), f16(rng, L, G * D)
+    c = filled_cache(k, v)
+    out = attn_decode(c, 0, dev(q), L, gate=dev(g))
+    assert_close(out, O.decode(q, k, v, L, gate=g), "decode L=262161")
+
+
 def test_decode_seq_len_zero_and_bounds():
     announce("decode L=0 / bounds")
     rng = np.random.default_rng(5)
