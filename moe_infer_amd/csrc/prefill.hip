@@ -61,6 +61,13 @@ __device__ __forceinline__ int qk_row_key(int m) {
   return (m & 0x13) | ((m & 4) << 1) | ((m & 8) >> 1);
 }
 
+// Buffer resource over a wave-uniform base: no stride, 2^31-1 bytes,
+// dword3 0x00020000 (32-bit data format, the value raw untyped buffer loads
+// take on CDNA).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
 __global__ void __launch_bounds__(256, 1)
 attn_prefill_kernel(PrefillArgs a) {
   extern __shared__ _Float16 lds[];
@@ -114,14 +121,19 @@ attn_prefill_kernel(PrefillArgs a) {
   for (int i = 0; i < 8; i++) acc[i] = f32x16{};
   float m = kNegBig, l = 0.f;
 
-  // Tiles move global -> LDS directly (global_load_lds_dwordx4: each lane's
-  // 16 bytes land at the wave's LDS base + 16 * lane), no staging registers.
+  // Tiles move global -> LDS directly (buffer_load_dwordx4 ... lds: each
+  // lane's 16 bytes land at the wave's LDS base + 16 * lane), no staging
+  // registers.  The buffer (MUBUF) form rather than global_load_lds: the
+  // compiler counts a global_load_lds as a possible LDS-counter event, and
+  // while one is pending it turns every LDS wait of the block into
+  // lgkmcnt(0), so the K/V fragment reads could not stay in flight across
+  // MFMAs.  Buffer bases are per tile (wave-uniform), offsets 32-bit.
   // A tile is 32 one-KiB pieces of K (two 32-key blocks of 16 KiB, each
   // block's two row halves u placed KU apart) and 32 pieces of V (eight 4 KiB
   // 8-key blocks, contiguous); wave w moves pieces 8w .. 8w+7 of each.
   const int lane16 = lane * 8;  // halves
-  const _Float16* kg = a.k + (int64_t)kvh * (32 * D) + lane16;
-  const _Float16* vg = a.v + (int64_t)kvh * (D * 8) + lane16;
+  const _Float16* kg = a.k + (int64_t)kvh * (32 * D);
+  const _Float16* vg = a.v + (int64_t)kvh * (D * 8);
   const int64_t kblk_stride = (int64_t)a.G * (32 * D);  // one 32-key block, all heads
   const int64_t vblk_stride = (int64_t)a.G * (D * 8);   // one 8-key block, all heads
   _Float16* const kbuf0 = lds;
@@ -131,17 +143,17 @@ attn_prefill_kernel(PrefillArgs a) {
     _Float16* ks = kbuf0 + (t & 1) * K_TILE_HALVES;
     const int i = 8 * w + pi;
     const int b = i >> 4, u = (i >> 3) & 1, pc = i & 7;
-    __builtin_amdgcn_global_load_lds(
-        (const void*)(kt + b * kblk_stride + (u * 8 + pc) * 512),
-        (__attribute__((address_space(3))) void*)(ks + b * KSUB + u * KU + pc * 512), 16, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        buf_rsrc(kt), (__attribute__((address_space(3))) void*)(ks + b * KSUB + u * KU + pc * 512), 16,
+        2 * (lane16 + b * (int)kblk_stride + (u * 8 + pc) * 512), 0, 0, 0);
   };
   auto load_v_piece = [&](int t, int pi) {
     const _Float16* vt = vg + (int64_t)(t * 8) * vblk_stride;
     _Float16* vs = vbuf0 + (t & 1) * V_TILE_HALVES;
     const int i = 8 * w + pi;
-    __builtin_amdgcn_global_load_lds(
-        (const void*)(vt + (i >> 2) * vblk_stride + (i & 3) * 512),
-        (__attribute__((address_space(3))) void*)(vs + i * 512), 16, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        buf_rsrc(vt), (__attribute__((address_space(3))) void*)(vs + i * 512), 16,
+        2 * (lane16 + (i >> 2) * (int)vblk_stride + (i & 3) * 512), 0, 0, 0);
   };
   auto load_k = [&](int t) {
     const _Float16* kt = kg + (int64_t)(t * 2) * kblk_stride;
@@ -150,9 +162,9 @@ attn_prefill_kernel(PrefillArgs a) {
     for (int pi = 0; pi < 8; pi++) {
       const int i = 8 * w + pi;
       const int b = i >> 4, u = (i >> 3) & 1, pc = i & 7;
-      __builtin_amdgcn_global_load_lds(
-          (const void*)(kt + b * kblk_stride + (u * 8 + pc) * 512),
-          (__attribute__((address_space(3))) void*)(ks + b * KSUB + u * KU + pc * 512), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          buf_rsrc(kt), (__attribute__((address_space(3))) void*)(ks + b * KSUB + u * KU + pc * 512), 16,
+          2 * (lane16 + b * (int)kblk_stride + (u * 8 + pc) * 512), 0, 0, 0);
     }
   };
   auto load_v = [&](int t) {
@@ -161,9 +173,9 @@ attn_prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int pi = 0; pi < 8; pi++) {
       const int i = 8 * w + pi;
-      __builtin_amdgcn_global_load_lds(
-          (const void*)(vt + (i >> 2) * vblk_stride + (i & 3) * 512),
-          (__attribute__((address_space(3))) void*)(vs + i * 512), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          buf_rsrc(vt), (__attribute__((address_space(3))) void*)(vs + i * 512), 16,
+          2 * (lane16 + (i >> 2) * (int)vblk_stride + (i & 3) * 512), 0, 0, 0);
     }
   };
   // Rows of the last tile past kv_len may hold stale data (NaN included):
@@ -221,11 +233,9 @@ attn_prefill_kernel(PrefillArgs a) {
 
   f16x8 pprev[2][2];
   bool pending = false;  // PV of the previous tile still to do
-  // QK^T of tile t: two 32-key sub-tiles, 16 k-steps each, the two chains
-  // interleaved.  With `dma`, the next tiles' global -> LDS pieces (K(t+1)
-  // piece i and V(t) piece i, i = 0..7) are issued between the MFMAs, so the
-  // issue stalls while the L2 -> LDS path drains overlap matrix work.
-  auto qk = [&](int t, f32x16 (&st)[2], bool dma) {
+  // QK^T of tile t (outside the steady state): two 32-key sub-tiles, 16
+  // k-steps each, the two chains interleaved.
+  auto qk = [&](int t, f32x16 (&st)[2]) {
     const _Float16* ks = kbuf0 + (t & 1) * K_TILE_HALVES;
     const _Float16* kr0 = ks + k_lds_off;
     const _Float16* kr1 = ks + KSUB + k_lds_off;
@@ -246,10 +256,6 @@ attn_prefill_kernel(PrefillArgs a) {
       }
       c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k], qf[k], c0, 0, 0, 0);
       c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kb[k], qf[k], c1, 0, 0, 0);
-      if (dma) {
-        if ((k & 1) == 0) load_k_piece(t + 1, k >> 1);
-        else load_v_piece(t, k >> 1);
-      }
     }
     st[0] = c0;
     st[1] = c1;
@@ -284,6 +290,89 @@ attn_prefill_kernel(PrefillArgs a) {
     rs = mi::sum_xor32(rs);
     l = l * alpha + rs;
   };
+  // Steady-state tile, one basic block in a fixed issue order (each slot
+  // closed by a scheduling barrier, so the compiler keeps it):
+  //  * QK(t): 16 k-steps of two MFMAs; K fragments are read from LDS
+  //    kRing k-steps ahead through a ring of registers (~8 reads in flight),
+  //    and one global -> LDS piece of the next tiles (K(t+1) piece k/2 on
+  //    even steps, V(t) piece k/2 on odd ones) is issued per step.  The last
+  //    four k-steps read the V fragments of PV step 0.
+  //  * PV(t-1): 4 steps of 8 MFMAs; after each MFMA the same ring slot is
+  //    refilled with the next step's fragment.  Tile t's softmax runs in
+  //    chunks between these MFMAs (it needs only QK(t), not PV(t-1)), and
+  //    writes P(t) into pprev once PV(t-1) has consumed the old P.
+  auto steady = [&](int t, float& alpha) {
+    const _Float16* ks = kbuf0 + (t & 1) * K_TILE_HALVES;
+    const _Float16* kr0 = ks + k_lds_off;
+    const _Float16* kr1 = ks + KSUB + k_lds_off;
+    const _Float16* vs = vbuf0 + ((t - 1) & 1) * V_TILE_HALVES + hl * (D * 8) + col * 8;
+    constexpr int kRing = 4;
+    f16x8 ka[kRing], kb[kRing], vf[8];
+    f32x16 c0 = f32x16{}, c1 = f32x16{};
+#pragma unroll
+    for (int k = 0; k < kRing; k++) {
+      ka[k] = *(const f16x8*)(kr0 + 256 * k);
+      kb[k] = *(const f16x8*)(kr1 + 256 * k);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k % kRing], qf[k], c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kb[k % kRing], qf[k], c1, 0, 0, 0);
+      if (k + kRing < 16) {
+        ka[k % kRing] = *(const f16x8*)(kr0 + 256 * (k + kRing));
+        kb[k % kRing] = *(const f16x8*)(kr1 + 256 * (k + kRing));
+      }
+      if (k >= 12) {
+        const int i0 = 2 * (k - 12);
+        vf[i0] = *(const f16x8*)(vs + i0 * 256);
+        vf[i0 + 1] = *(const f16x8*)(vs + (i0 + 1) * 256);
+      }
+      if ((k & 1) == 0) load_k_piece(t + 1, k >> 1);
+      else load_v_piece(t, k >> 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    f16x8 pnew[2][2];
+    float mt = 0.f, mnew = 0.f, rs = 0.f;
+#pragma unroll
+    for (int st4 = 0; st4 < 4; st4++) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[i], pprev[st4 >> 1][st4 & 1], acc[i], 0, 0, 0);
+        if (st4 + 1 < 4) vf[i] = *(const f16x8*)(vs + 2 * (st4 + 1) * (D * 8) + i * 256);
+        const int slot = st4 * 8 + i;
+        if (slot == 2) {
+          mt = c0[0];
+#pragma unroll
+          for (int e = 1; e < 16; e++) mt = fmaxf(mt, c0[e]);
+        } else if (slot == 3) {
+#pragma unroll
+          for (int e = 0; e < 16; e++) mt = fmaxf(mt, c1[e]);
+          mt = mi::max_xor32(mt) * c2;
+          mnew = (mt > m + kLazy) ? mt : m;
+          alpha = __builtin_amdgcn_exp2f(m - mnew);
+          m = mnew;
+        } else if (slot >= 4 && slot < 20) {
+          const int e0 = 2 * (slot - 4);  // scores e0, e0 + 1 of the 32
+          const int sub = e0 >> 4, ee = e0 & 15;
+          const float sa = sub ? c1[ee] : c0[ee], sb = sub ? c1[ee + 1] : c0[ee + 1];
+          const float pa = __builtin_amdgcn_exp2f(fmaf(sa, c2, -mnew));
+          const float pb = __builtin_amdgcn_exp2f(fmaf(sb, c2, -mnew));
+          rs += pa + pb;
+          pnew[sub][ee >> 3][ee & 7] = (_Float16)pa;
+          pnew[sub][ee >> 3][(ee & 7) + 1] = (_Float16)pb;
+        } else if (slot == 20) {
+          rs = mi::sum_xor32(rs);
+          l = l * alpha + rs;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int a2 = 0; a2 < 2; a2++)
+#pragma unroll
+      for (int b2 = 0; b2 < 2; b2++) pprev[a2][b2] = pnew[a2][b2];
+  };
   for (int t = 0; t < nt; t++) {
     const int key0 = t * BK;
     const bool active = key0 <= wave_last;
@@ -291,25 +380,12 @@ attn_prefill_kernel(PrefillArgs a) {
     float alpha = 1.f;
     f32x16 st[2];
     if (active && pending && !diag) {
-      // Steady state (a later tile holds this wave's diagonal, so t + 1 < nt),
-      // one basic block: QK(t) with the next tiles' DMA issue spread over its
-      // MFMAs, then PV(t-1), which is independent of tile t's softmax, so
-      // MFMA and VALU issue side by side.
-      qk(t, st, true);
-      f16x8 pcur[2][2];
-#pragma unroll
-      for (int a2 = 0; a2 < 2; a2++)
-#pragma unroll
-        for (int b2 = 0; b2 < 2; b2++) pcur[a2][b2] = pprev[a2][b2];
-      pv(t - 1, pcur);
-      softmax(st, alpha);
-      // LLVM's single-wave MFMA / LDS interleave strategy for this block
-      // (measured ~6% faster than the default schedule at C4).
-      __builtin_amdgcn_iglp_opt(1);
+      // Steady state: a later tile holds this wave's diagonal, so t + 1 < nt.
+      steady(t, alpha);
     } else {
       if (t + 1 < nt) load_k(t + 1);
       load_v(t);
-      if (active) qk(t, st, false);
+      if (active) qk(t, st);
       if (pending) pv(t - 1, pprev);
       if (active) {
         if (diag) {  // causal mask: key (key0 + 16 s2 + 8 hl + e7) <= qpos
