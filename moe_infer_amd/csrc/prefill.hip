@@ -132,6 +132,9 @@ attn_prefill_kernel(PrefillArgs a) {
   // block's two row halves u placed KU apart) and 32 pieces of V (eight 4 KiB
   // 8-key blocks, contiguous); wave w moves pieces 8w .. 8w+7 of each.
   const int lane16 = lane * 8;  // halves
+  // The wave index as a scalar, so that the copies' LDS addresses (M0) are
+  // computed on the scalar unit.
+  const int wu = __builtin_amdgcn_readfirstlane(w);
   const _Float16* kg = a.k + (int64_t)kvh * (32 * D);
   const _Float16* vg = a.v + (int64_t)kvh * (D * 8);
   const int64_t kblk_stride = (int64_t)a.G * (32 * D);  // one 32-key block, all heads
@@ -141,7 +144,7 @@ attn_prefill_kernel(PrefillArgs a) {
   auto load_k_piece = [&](int t, int pi) {
     const _Float16* kt = kg + (int64_t)(t * 2) * kblk_stride;
     _Float16* ks = kbuf0 + (t & 1) * K_TILE_HALVES;
-    const int i = 8 * w + pi;
+    const int i = 8 * wu + pi;
     const int b = i >> 4, u = (i >> 3) & 1, pc = i & 7;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         buf_rsrc(kt), (__attribute__((address_space(3))) void*)(ks + b * KSUB + u * KU + pc * 512), 16,
@@ -150,7 +153,7 @@ attn_prefill_kernel(PrefillArgs a) {
   auto load_v_piece = [&](int t, int pi) {
     const _Float16* vt = vg + (int64_t)(t * 8) * vblk_stride;
     _Float16* vs = vbuf0 + (t & 1) * V_TILE_HALVES;
-    const int i = 8 * w + pi;
+    const int i = 8 * wu + pi;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         buf_rsrc(vt), (__attribute__((address_space(3))) void*)(vs + i * 512), 16,
         2 * (lane16 + (i >> 2) * (int)vblk_stride + (i & 3) * 512), 0, 0, 0);
@@ -160,7 +163,7 @@ attn_prefill_kernel(PrefillArgs a) {
     _Float16* ks = kbuf0 + (t & 1) * K_TILE_HALVES;
 #pragma unroll
     for (int pi = 0; pi < 8; pi++) {
-      const int i = 8 * w + pi;
+      const int i = 8 * wu + pi;
       const int b = i >> 4, u = (i >> 3) & 1, pc = i & 7;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           buf_rsrc(kt), (__attribute__((address_space(3))) void*)(ks + b * KSUB + u * KU + pc * 512), 16,
@@ -172,7 +175,7 @@ attn_prefill_kernel(PrefillArgs a) {
     _Float16* vs = vbuf0 + (t & 1) * V_TILE_HALVES;
 #pragma unroll
     for (int pi = 0; pi < 8; pi++) {
-      const int i = 8 * w + pi;
+      const int i = 8 * wu + pi;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           buf_rsrc(vt), (__attribute__((address_space(3))) void*)(vs + i * 512), 16,
           2 * (lane16 + (i >> 2) * (int)vblk_stride + (i & 3) * 512), 0, 0, 0);
