@@ -483,9 +483,11 @@ attn_split_kernel(SplitArgs a, X x) {
       for (int u = 0; u < 2; u++)
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          const float p = exp2f(st[u][e] - mnew);
-          rs += p;
-          pf[4 * u + e] = (_Float16)p;
+          // The row sum adds the f16 weights the PV MFMA uses, so that the
+          // normalised weights sum to one.
+          const _Float16 ph = (_Float16)exp2f(st[u][e] - mnew);
+          rs += (float)ph;
+          pf[4 * u + e] = ph;
         }
       rs = mi::sum_rows(rs);
       l[cb] = l[cb] * alpha + rs;

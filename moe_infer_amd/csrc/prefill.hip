@@ -269,7 +269,9 @@ attn_prefill_kernel(PrefillArgs a) {
   // only when the tile's max exceeds it by more than kLazy (base-2 units):
   // P = 2^(s - m) then stays below 2^kLazy (well inside f16 and f32), the
   // final normalisation divides by l accumulated against the same m, and
-  // the O rescale (alpha != 1) becomes rare.
+  // the O rescale (alpha != 1) becomes rare.  The row sum adds the f16
+  // weights the PV MFMA uses (v_dot2_f32_f16 against (1, 1), f32
+  // accumulation), so that the normalised weights sum to one.
   constexpr float kLazy = 8.f;
   auto softmax = [&](f32x16 (&st)[2], float& alpha) {
     float mt = st[0][0];
@@ -285,10 +287,12 @@ attn_prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int sub = 0; sub < 2; sub++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(st[sub][e], c2, -mnew));
-        rs += p;
-        pprev[sub][e >> 3][e & 7] = (_Float16)p;
+      for (int e = 0; e < 16; e += 2) {
+        const f16x2 ph = {(_Float16)__builtin_amdgcn_exp2f(fmaf(st[sub][e], c2, -mnew)),
+                          (_Float16)__builtin_amdgcn_exp2f(fmaf(st[sub][e + 1], c2, -mnew))};
+        rs = __builtin_amdgcn_fdot2(ph, f16x2{1.f16, 1.f16}, rs, false);
+        pprev[sub][e >> 3][e & 7] = ph[0];
+        pprev[sub][e >> 3][(e & 7) + 1] = ph[1];
       }
     rs = mi::sum_xor32(rs);
     l = l * alpha + rs;
@@ -359,11 +363,11 @@ attn_prefill_kernel(PrefillArgs a) {
           const int e0 = 2 * (slot - 4);  // scores e0, e0 + 1 of the 32
           const int sub = e0 >> 4, ee = e0 & 15;
           const float sa = sub ? c1[ee] : c0[ee], sb = sub ? c1[ee + 1] : c0[ee + 1];
-          const float pa = __builtin_amdgcn_exp2f(fmaf(sa, c2, -mnew));
-          const float pb = __builtin_amdgcn_exp2f(fmaf(sb, c2, -mnew));
-          rs += pa + pb;
-          pnew[sub][ee >> 3][ee & 7] = (_Float16)pa;
-          pnew[sub][ee >> 3][(ee & 7) + 1] = (_Float16)pb;
+          const f16x2 ph = {(_Float16)__builtin_amdgcn_exp2f(fmaf(sa, c2, -mnew)),
+                            (_Float16)__builtin_amdgcn_exp2f(fmaf(sb, c2, -mnew))};
+          rs = __builtin_amdgcn_fdot2(ph, f16x2{1.f16, 1.f16}, rs, false);
+          pnew[sub][ee >> 3][ee & 7] = ph[0];
+          pnew[sub][ee >> 3][(ee & 7) + 1] = ph[1];
         } else if (slot == 20) {
           rs = mi::sum_xor32(rs);
           l = l * alpha + rs;
