@@ -222,13 +222,34 @@ def main():
             "graph_step_us_per_layer": ms_graph * 1000 / LAYERS,
             "graph_gbps": C2_BYTES / (ms_graph * 1e6 / LAYERS), "graph_matches_eager": graph_ok,
         }
+        # Attend-only calls at other context lengths (the split plan depends on
+        # the length), over 4 layers of 50000 rows (more than the last-level cache).
+        del cache
+        sweep_lens = (8193, 32769, 50000)
+        scache = mi.Cache(num_layers=4, capacity=max(sweep_lens))
+        for layer in range(4):
+            k = randn(max(sweep_lens), G * D, seed=1200 + layer)
+            v = randn(max(sweep_lens), G * D, seed=1300 + layer)
+            mi.kv_cache_append(scache, layer, k, v, 0)
+            del k, v
+        sweep = {}
+        for sl in sweep_lens:
+            def attend_len(sl=sl):
+                for layer in range(4):
+                    mi.attn_decode(scache, layer, qs[layer], sl, gate=gs[layer], out=outs[layer])
+            ms_sl = timed(attend_len, args.steps, args.warmup, backlog_ms=args.steps * 4 * 0.3 + 20)
+            _lib.prof_enable(False)
+            sweep[str(sl)] = {"us_per_call": ms_sl * 1000 / 4,
+                              "gbps": (sl * G * D * 4 + 3 * H * D * 2) / (ms_sl * 1e6 / 4)}
+        rec["decode"]["attend_by_ctx"] = sweep
+        del scache
         print(f"[bench] decode step {us_layer:.2f} us/layer (attend only "
               f"{ms_attend * 100:.2f}, from projections {ms_proj * 100:.2f}: split "
               f"{proj_split_us:.2f} combine {proj_comb_us:.2f}; two calls {ms_two * 100:.2f}, "
               f"rope kernel {rope_us:.2f}) split {split_us:.2f} us combine {comb_us:.2f} us; "
-              f"graph replay {ms_graph * 100:.2f} us/layer (matches eager: {graph_ok})",
+              f"graph replay {ms_graph * 100:.2f} us/layer (matches eager: {graph_ok}); "
+              + ", ".join(f"ctx {k_} {v_['us_per_call']:.2f} us" for k_, v_ in sweep.items()),
               file=sys.stderr, flush=True)
-        del cache
 
     # --------------------------------------------------------------- C4 prefill
     if not only or "prefill" in only:
