@@ -28,9 +28,11 @@ constexpr int D = mi::kHeadDim;
 constexpr int BQ = 128;        // queries per workgroup
 constexpr int BK = 64;         // keys per LDS tile
 // K tile in LDS: two 32-key blocks copied verbatim from the cache layout
-// (mi::k_offset), each block's two row halves (u) separated by 128 bytes so
-// that the 16 lanes of an A-operand read hit distinct banks.
-constexpr int KU = 16 * D + 64;             // one u half + pad (halves)
+// (mi::k_offset), unpadded.  An A-operand read then hits each LDS bank once
+// per 16-byte slot (rocprofv3 SQ_LDS_BANK_CONFLICT: 0); with the two row
+// halves u of a block 128 bytes out of step, half of that read's LDS cycles
+// were bank conflicts on gfx950.
+constexpr int KU = 16 * D;                  // one u half (halves)
 constexpr int KSUB = 2 * KU;                // one 32-key block
 constexpr int K_TILE_HALVES = 2 * KSUB;
 constexpr int V_TILE_HALVES = BK * D;  // 8 blocks of [D][8]
@@ -129,7 +131,7 @@ attn_prefill_kernel(PrefillArgs a) {
   // lgkmcnt(0), so the K/V fragment reads could not stay in flight across
   // MFMAs.  Buffer bases are per tile (wave-uniform), offsets 32-bit.
   // A tile is 32 one-KiB pieces of K (two 32-key blocks of 16 KiB, each
-  // block's two row halves u placed KU apart) and 32 pieces of V (eight 4 KiB
+  // block's two row halves u, KU apart) and 32 pieces of V (eight 4 KiB
   // 8-key blocks, contiguous); wave w moves pieces 8w .. 8w+7 of each.
   const int lane16 = lane * 8;  // halves
   // The wave index as a scalar, so that the copies' LDS addresses (M0) are
