@@ -342,7 +342,12 @@ attn_prefill_kernel(PrefillArgs a) {
       __builtin_amdgcn_sched_barrier(0);
     }
     f16x8 pnew[2][2];
-    float mt = 0.f, mnew = 0.f, rs = 0.f;
+    // The weights use the running reference max m as it stands: no row max
+    // is taken in the steady state.  They are valid while none reaches 2^15
+    // (f16 range; each weight is at most its lane's sum); otherwise, rarely,
+    // the tile is redone below with the new row max.
+    float rs = 0.f;
+    bool ovf = false;
 #pragma unroll
     for (int st4 = 0; st4 < 4; st4++) {
 #pragma unroll
@@ -350,33 +355,46 @@ attn_prefill_kernel(PrefillArgs a) {
         acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[i], pprev[st4 >> 1][st4 & 1], acc[i], 0, 0, 0);
         if (st4 + 1 < 4) vf[i] = *(const f16x8*)(vs + 2 * (st4 + 1) * (D * 8) + i * 256);
         const int slot = st4 * 8 + i;
-        if (slot == 2) {
-          mt = c0[0];
-#pragma unroll
-          for (int e = 1; e < 16; e++) mt = fmaxf(mt, c0[e]);
-        } else if (slot == 3) {
-#pragma unroll
-          for (int e = 0; e < 16; e++) mt = fmaxf(mt, c1[e]);
-          mt = mi::max_xor32(mt) * c2;
-          mnew = (mt > m + kLazy) ? mt : m;
-          alpha = __builtin_amdgcn_exp2f(m - mnew);
-          m = mnew;
-        } else if (slot >= 4 && slot < 20) {
-          const int e0 = 2 * (slot - 4);  // scores e0, e0 + 1 of the 32
+        if (slot >= 2 && slot < 18) {
+          const int e0 = 2 * (slot - 2);  // scores e0, e0 + 1 of the 32
           const int sub = e0 >> 4, ee = e0 & 15;
           const float sa = sub ? c1[ee] : c0[ee], sb = sub ? c1[ee + 1] : c0[ee + 1];
-          const f16x2 ph = {(_Float16)__builtin_amdgcn_exp2f(fmaf(sa, c2, -mnew)),
-                            (_Float16)__builtin_amdgcn_exp2f(fmaf(sb, c2, -mnew))};
+          const f16x2 ph = {(_Float16)__builtin_amdgcn_exp2f(fmaf(sa, c2, -m)),
+                            (_Float16)__builtin_amdgcn_exp2f(fmaf(sb, c2, -m))};
           rs = __builtin_amdgcn_fdot2(ph, f16x2{1.f16, 1.f16}, rs, false);
           pnew[sub][ee >> 3][ee & 7] = ph[0];
           pnew[sub][ee >> 3][(ee & 7) + 1] = ph[1];
-        } else if (slot == 20) {
+        } else if (slot == 18) {
+          ovf = !(rs < 32768.f);  // also inf / NaN
           rs = mi::sum_xor32(rs);
-          l = l * alpha + rs;
         }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    if (__ballot(ovf)) {  // wave-uniform: a row max moved up by 15 or more
+      float mt = c0[0];
+#pragma unroll
+      for (int e = 1; e < 16; e++) mt = fmaxf(mt, c0[e]);
+#pragma unroll
+      for (int e = 0; e < 16; e++) mt = fmaxf(mt, c1[e]);
+      mt = mi::max_xor32(mt) * c2;
+      const float mnew = fmaxf(m, mt);
+      alpha = __builtin_amdgcn_exp2f(m - mnew);
+      m = mnew;
+      rs = 0.f;
+#pragma unroll
+      for (int e = 0; e < 32; e += 2) {
+        const int sub = e >> 4, ee = e & 15;
+        const float sa = sub ? c1[ee] : c0[ee], sb = sub ? c1[ee + 1] : c0[ee + 1];
+        const f16x2 ph = {(_Float16)__builtin_amdgcn_exp2f(fmaf(sa, c2, -m)),
+                          (_Float16)__builtin_amdgcn_exp2f(fmaf(sb, c2, -m))};
+        rs = __builtin_amdgcn_fdot2(ph, f16x2{1.f16, 1.f16}, rs, false);
+        pnew[sub][ee >> 3][ee & 7] = ph[0];
+        pnew[sub][ee >> 3][(ee & 7) + 1] = ph[1];
+      }
+      rs = mi::sum_xor32(rs);
+    }
+    l = l * alpha + rs;
 #pragma unroll
     for (int a2 = 0; a2 < 2; a2++)
 #pragma unroll
