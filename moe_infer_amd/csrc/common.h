@@ -56,6 +56,15 @@ __device__ __forceinline__ void sync_lds() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// The sigmoid output gate, x * sigmoid(g) = x / (1 + e^-g) (reference
+// sigmoid_gate_inplace, src/math_util.rs:264-269), with the hardware base-2
+// exponential and reciprocal (v_exp_f32, v_rcp_f32: about 1 ulp each)
+// instead of the correctly rounded library expf and an IEEE division.
+// g -> -inf gives 0, g -> +inf gives x.
+__device__ __forceinline__ float gate_mul(float x, float g) {
+  return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * kLog2e));
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float((uint32_t)b << 16);
 }

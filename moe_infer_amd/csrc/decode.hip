@@ -673,11 +673,11 @@ attn_combine_kernel(CombineArgs a) {
     const int64_t oidx = (((int64_t)s * a.nq + tok) * a.H + hq) * D + d0 + t;
     if (a.gate) {
       const float gv = (float)a.gate[oidx];
-      r *= 1.f / (1.f + expf(-gv));
+      r = mi::gate_mul(r, gv);
     } else if (a.gate32) {
       const float gv =
           a.gate32[(((int64_t)s * a.nq + tok) * a.H + hq) * (2 * D) + D + d0 + t];
-      r *= 1.f / (1.f + expf(-gv));
+      r = mi::gate_mul(r, gv);
     }
     a.out[oidx] = (_Float16)r;
   }
@@ -735,7 +735,7 @@ attn_combine_flat_kernel(CombineArgs a) {
   if (bad) r = __builtin_nanf("");
   const int hq = kvh * 8 + c;
   const int64_t oidx = ((int64_t)s * a.H + hq) * D + d;
-  if (a.gate) r *= 1.f / (1.f + expf(-(float)a.gate[oidx]));
+  if (a.gate) r = mi::gate_mul(r, (float)a.gate[oidx]);
   a.out[oidx] = (_Float16)r;
 }
 

@@ -447,6 +447,17 @@ attn_prefill_kernel(PrefillArgs a) {
   // wave instruction), the gate read the same way; the accumulator layout
   // would otherwise make each lane store 8 bytes into 32 rows 8 KiB apart.
   __syncthreads();  // every wave is done with the K/V tiles
+  // The gate rows are loaded first, so that their latency overlaps the
+  // staging of O (lane: columns dc .. dc+7 of rows 2 st + hl).
+  const int dc = 8 * (lane & 31);  // this lane's 8 columns of a row
+  f16x8 gv[16];
+  if (a.gate) {
+#pragma unroll
+    for (int st = 0; st < 16; st++) {
+      const int qr = q0 + 32 * w + 2 * st + hl;
+      gv[st] = qr < a.n ? *(const f16x8*)(a.gate + ((int64_t)qr * a.H + hq) * D + dc) : f16x8{};
+    }
+  }
   float* ob = (float*)lds + w * 32 * O_ROW;
   const float inv = (l > 0.f) ? 1.f / l : 0.f;
 #pragma unroll
@@ -459,8 +470,7 @@ attn_prefill_kernel(PrefillArgs a) {
       *(f32x4*)(ob + col * O_ROW + i * 32 + 8 * e4 + 4 * hl) = o;
     }
   mi::sync_lds();
-  const int dc = 8 * (lane & 31);  // this lane's 8 columns of a row
-#pragma unroll 4
+#pragma unroll
   for (int st = 0; st < 16; st++) {
     const int r = 2 * st + hl;  // query row of the wave
     const int qr = q0 + 32 * w + r;
@@ -475,11 +485,10 @@ attn_prefill_kernel(PrefillArgs a) {
       y[4 + e] = (_Float16)x1[e];
     }
     if (a.gate) {
-      const f16x8 gv = *(const f16x8*)(a.gate + obase);
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        y[e] = (_Float16)(x0[e] / (1.f + expf(-(float)gv[e])));
-        y[4 + e] = (_Float16)(x1[e] / (1.f + expf(-(float)gv[4 + e])));
+        y[e] = (_Float16)mi::gate_mul(x0[e], (float)gv[st][e]);
+        y[4 + e] = (_Float16)mi::gate_mul(x1[e], (float)gv[st][4 + e]);
       }
     }
     *(f16x8*)(a.out + obase) = y;
