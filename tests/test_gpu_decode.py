@@ -226,3 +226,27 @@ def test_graph_replay_of_steps_matches_eager():
             assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"replay {r}"
     assert_close(out1, O.decode(host(q), k[:L + 1], v[:L + 1], L + 1, gate=host(g)),
                  "graph step vs oracle")
+
+
+def test_gate_extremes_decode_and_prefill():
+    """Gate logits far in both tails (sigmoid -> 0 and -> 1, including values
+    whose exponential overflows f32) and around 0, for the decode combine and
+    the prefill epilogue, against the oracle's x / (1 + e^-g)."""
+    announce("gate extremes")
+    from moe_infer_amd import attn_prefill
+    rng = np.random.default_rng(21)
+    L = 300
+    k, v = f16(rng, L, G * D), f16(rng, L, G * D)
+    grid = np.array([-60000.0, -200.0, -90.0, -20.0, -3.0, -0.5, 0.0, 0.5, 3.0, 20.0, 90.0,
+                     200.0, 60000.0], dtype=np.float32)
+    q = f16(rng, H * D)
+    g = np.resize(grid, H * D).astype(np.float16)
+    c = filled_cache(k, v)
+    out = attn_decode(c, 0, dev(q), L, gate=dev(g))
+    assert_close(out, O.decode(q, k, v, L, gate=g), "decode gate extremes")
+    n = 40
+    qn, kn, vn = f16(rng, n, H, D), f16(rng, n, G * D), f16(rng, n, G * D)
+    gn = np.resize(grid, n * H * D).reshape(n, H, D).astype(np.float16)
+    c2 = Cache(num_layers=1, capacity=n)
+    outp = attn_prefill(c2, 0, dev(qn), dev(kn), dev(vn), 0, gate=dev(gn))
+    assert_close(outp, O.causal(qn, kn, vn, 0, gate=gn), "prefill gate extremes")
