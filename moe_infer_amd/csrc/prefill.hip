@@ -406,8 +406,11 @@ attn_prefill_kernel(PrefillArgs a) {
     const bool diag = key0 + BK - 1 > wave_first;
     float alpha = 1.f;
     f32x16 st[2];
-    if (active && pending && !diag) {
-      // Steady state: a later tile holds this wave's diagonal, so t + 1 < nt.
+    // Steady state: not the wave's first or diagonal tile, and not the last
+    // tile (the steady schedule copies K(t+1)).  A wave whose queries are all
+    // past n has its diagonal beyond the last tile, so `!diag` alone does not
+    // imply t + 1 < nt: K(nt) can lie past the end of the allocation.
+    if (active && pending && !diag && t + 1 < nt) {
       steady(t, alpha);
     } else {
       if (t + 1 < nt) load_k(t + 1);

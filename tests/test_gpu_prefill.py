@@ -79,3 +79,23 @@ def test_prefill_rising_scores():
     for i in [0, 63, 64, 200, 255, 256, 383, 384, 447, 500, 511]:
         ref = O.decode(q[i].ravel(), k, v, i + 1)
         assert_close(out[i], ref, f"rising scores row {i}")
+
+
+@pytest.mark.parametrize("past,n", [(308, 141), (200, 56), (31, 162)])
+def test_prefill_cache_full_to_capacity(past, n):
+    """The cache holds exactly past + n rows, rounded up to 256, and the
+    last 64-key tile ends at the allocation's end.  Waves whose queries
+    are all past n must not copy a K tile beyond it (they once did, in
+    the steady-state schedule)."""
+    announce(f"prefill full cache past={past} n={n}")
+    rng = np.random.default_rng(past + 3 * n)
+    kp, vp = f16(rng, past, G * D), f16(rng, past, G * D)
+    q, k, v = f16(rng, n, H, D), f16(rng, n, G * D), f16(rng, n, G * D)
+    c = Cache(num_layers=1, capacity=past + n)
+    assert c.capacity == (past + n + 255) // 256 * 256
+    if past:
+        c.upload(0, kp, vp)
+        c.set_pos(past)
+    out = attn_prefill(c, 0, dev(q), dev(k), dev(v), past)
+    ref = O.causal(q, np.concatenate([kp, k]), np.concatenate([vp, v]), past)
+    assert_close(out, ref, f"prefill full cache past={past} n={n}")
