@@ -27,7 +27,7 @@ def _filled(rng, past, capacity):
     return c, kp, vp
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(16))
 def test_prefill_random_shapes(seed):
     rng = np.random.default_rng(1000 + seed)
     past = int(rng.integers(0, 1200))
