@@ -56,7 +56,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is "
-                          "designed but not built (DESIGN.md)", "n_gpus": args.gpus}))
+                          "designed (shard by KV head, then by context) but not built", "n_gpus": args.gpus}))
         sys.exit(2)
 
     import numpy as np
