@@ -12,7 +12,18 @@
  *   - Work is enqueued on the caller's stream (a hipStream_t passed as void*;
  *     NULL is the legacy default stream) and is asynchronous unless the name
  *     ends in _sync.  A handle is not internally synchronised: use one handle
- *     per thread (the reference's pyclasses are `unsendable`).
+ *     per thread (the reference's pyclasses are `unsendable`).  The decode,
+ *     step and verify calls of one handle share its split-K workspace, so
+ *     issue them on one stream (or order the streams with events): two of
+ *     them running concurrently on different streams race on it.
+ *   - Graph capture: the calls allocate and clear nothing once the cache and
+ *     the handle's workspace are large enough, so they can be captured.  A
+ *     call that would have to grow either while its stream is capturing
+ *     returns MI_ERR_INVALID_ARG; make one eager call of the largest size
+ *     (or mi_kv_reserve) first.  A workspace replaced by a larger one is
+ *     kept until mi_kv_destroy, so graphs captured earlier stay valid; cache
+ *     growth (mi_kv_reserve, or an append past capacity) moves the K/V
+ *     buffers and invalidates every graph captured on the handle.
  *   - A handle belongs to the device that is current at mi_kv_create; calls
  *     that allocate or launch work on it return MI_ERR_INVALID_ARG unless
  *     that device is current.

@@ -9,10 +9,10 @@ from . import _lib
 from .attention import (attn_decode, attn_decode_ragged, attn_prefill, attn_step, attn_step_proj,
                         attn_verify, kv_cache_append, kv_pack, matvec_bf16, matvec_q4,
                         qk_norm_rope_append, ragged_workspace)
-from .engine import Engine, EngineSnapshot, record_engine_telemetry
+from .engine import Engine, EngineInterrupted, EngineSnapshot, record_engine_telemetry
 from .kv_cache import Cache
 
-__all__ = ["Cache", "Engine", "EngineSnapshot", "record_engine_telemetry", "attn_decode",
+__all__ = ["Cache", "Engine", "EngineInterrupted", "EngineSnapshot", "record_engine_telemetry", "attn_decode",
            "attn_decode_ragged", "attn_prefill", "attn_step", "attn_step_proj", "attn_verify",
            "kv_cache_append", "kv_pack", "matvec_bf16", "matvec_q4", "qk_norm_rope_append",
            "ragged_workspace", "_lib"]

@@ -161,6 +161,9 @@ struct mi_kv {
   // Split-K decode / verify partials, grown on demand and kept for reuse.
   void* ws = nullptr;
   size_t ws_bytes = 0;
+  // Workspaces replaced by a larger one; freed at mi_kv_destroy (graphs
+  // captured before the growth still address them).
+  std::vector<void*> ws_retired;
 };
 
 namespace mi {
@@ -169,8 +172,12 @@ namespace mi {
 mi_status check_kv(const mi_kv* kv);
 // check_kv and 0 <= layer < layers.
 mi_status check_layer(const mi_kv* kv, int32_t layer);
-// Ensures the handle's workspace holds at least `bytes` (synchronous grow).
-mi_status kv_workspace(mi_kv* kv, size_t bytes, void** ws);
+// Ensures the handle's workspace holds at least `bytes` (synchronous grow;
+// refused while `stream` is capturing a graph).
+mi_status kv_workspace(mi_kv* kv, size_t bytes, hipStream_t stream, void** ws);
+// Grows the cache to at least `rows` rows (mi_kv_reserve), refused while
+// `stream` is capturing a graph.
+mi_status kv_grow(mi_kv* kv, int64_t rows, hipStream_t stream);
 // Enqueues the row copy of kv_cache_append_n on `stream` (no len update).
 mi_status kv_append_rows(mi_kv* kv, int32_t layer, const _Float16* k,
                          const _Float16* v, int64_t pos, int32_t n,

@@ -32,6 +32,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "plan.h"
 
 namespace {
 
@@ -585,7 +586,7 @@ struct CombineArgs {
 // denominator is zero (the reference's `sum > 0` guard and zero-filled
 // output, math_util.rs:357, 372), then * sigmoid(gate).
 constexpr int kCombineSlice = 16;
-constexpr int kMaxChunks = 1024;
+constexpr int kMaxChunks = mi::kMaxSplitChunks;
 
 extern "C" __device__ float __ockl_wfred_max_f32(float);
 extern "C" __device__ float __ockl_wfred_add_f32(float);
@@ -780,61 +781,16 @@ int env_int(const char* name, int dflt) {
 // defaults are the tuned values): MI_ATTN_SPLIT_GH=1 puts one KV head per
 // workgroup, MI_ATTN_SPLIT_WGS sets the target workgroup count,
 // MI_ATTN_SPLIT_CHUNK fixes the keys per chunk.
-struct SplitKnobs {
-  int gh, wgs, chunk;
-};
-const SplitKnobs& split_knobs() {
-  static const SplitKnobs k{env_int("MI_ATTN_SPLIT_GH", 2),
-                            std::max(1, env_int("MI_ATTN_SPLIT_WGS", 256)),
-                            std::max(0, env_int("MI_ATTN_SPLIT_CHUNK", 0))};
+const mi::SplitKnobs& split_knobs() {
+  static const mi::SplitKnobs k{env_int("MI_ATTN_SPLIT_GH", 2),
+                                std::max(1, env_int("MI_ATTN_SPLIT_WGS", 256)),
+                                std::max(0, env_int("MI_ATTN_SPLIT_CHUNK", 0))};
   return k;
 }
 
-struct SplitPlan {
-  int nwh, gh, ncb, chunk, max_chunks;
-};
-
-// Kernel variant and chunking of one split launch.  Keys per chunk (per
-// head): enough workgroups to cover 256 CUs about once (K/V of one key and
-// head is 1 KiB, so a 128-key chunk of two heads moves 256 KiB and leaves
-// one 8 KiB partial per head and query token), at least one 32-key tile per
-// wave, at most 2048 keys (ragged batches balance better with more
-// workgroups), and at most kMaxChunks chunks per sequence.
+using mi::SplitPlan;
 SplitPlan plan_split(int64_t max_len, int64_t batch, int G, int nq) {
-  SplitPlan p;
-  p.ncb = nq <= 2 ? 1 : 2;
-  if (p.ncb == 2) {  // 32 columns: 4 waves, one head (registers and LDS)
-    p.nwh = 4;
-    p.gh = 1;
-  } else if (G % 2 == 0 && split_knobs().gh == 2) {
-    p.nwh = 4;
-    p.gh = 2;
-  } else {
-    p.nwh = 8;
-    p.gh = 1;
-  }
-  const int64_t step = 32 * p.nwh;
-  const int64_t target_wgs = split_knobs().wgs;
-  int64_t chunk = split_knobs().chunk;
-  if (chunk <= 0) {
-    chunk = (batch * G * max_len + p.gh * target_wgs - 1) / (p.gh * target_wgs);
-    if (chunk > 2048) chunk = 2048;
-  }
-  const int64_t min_chunk = (max_len + kMaxChunks - 1) / kMaxChunks;
-  if (chunk < min_chunk) chunk = min_chunk;
-  // Chunks are whole 32-key tiles; the waves of a workgroup take its tiles
-  // round-robin.  Decode rounds chunks to 32 keys: rounding up to 32 * NWH
-  // would leave up to half the CUs idle just above a power of two (ctx
-  // 32769: 129 workgroups instead of 256, 21.0 against 18.1 us per call).
-  // The 32-column verify keeps whole wave rounds (measured ~1 us faster at
-  // 65540 rows: 206 workgroups of 20 tiles against 242 of 17).
-  const int64_t gran = p.ncb == 2 ? step : 32;
-  chunk = (chunk + gran - 1) / gran * gran;
-  if (chunk < gran) chunk = gran;  // also for max_len == 0
-  p.chunk = (int)chunk;
-  p.max_chunks = (int)((max_len + chunk - 1) / chunk);
-  if (p.max_chunks < 1) p.max_chunks = 1;
-  return p;
+  return mi::plan_split(max_len, batch, G, nq, split_knobs());
 }
 
 template <int NWH, int NCB, int GH, typename X = NoProj, bool FLAT = false>
@@ -992,7 +948,7 @@ mi_status cache_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float
     const int64_t rows = past_pos + t0 + nq;  // rows the last token of this group sees
     const SplitPlan plan = plan_split(rows, 1, kv->G, nq);
     void* ws;
-    MI_TRY(mi::kv_workspace(kv, split_workspace_bytes(1, kv->G, plan.max_chunks, nq), &ws));
+    MI_TRY(mi::kv_workspace(kv, split_workspace_bytes(1, kv->G, plan.max_chunks, nq), stream, &ws));
     const int64_t qoff = (int64_t)t0 * kv->H * D;
     AppendRows app;
     if (k_new) {
@@ -1038,7 +994,7 @@ extern "C" mi_status mi_attn_step(mi_kv* kv, int32_t layer, const mi_f16* q,
   MI_TRY(mi::check_layer(kv, layer));
   if (!q || !k || !v || !out) return mi::fail(MI_ERR_INVALID_ARG, "null q/k/v/out");
   if (pos < 0) return mi::fail(MI_ERR_OUT_OF_RANGE, "pos=%lld", (long long)pos);
-  if (pos + 1 > kv->cap) MI_TRY(mi_kv_reserve(kv, pos + 1));
+  MI_TRY(mi::kv_grow(kv, pos + 1, (hipStream_t)stream));
   MI_TRY(cache_attend(kv, layer, (const _Float16*)q, (const _Float16*)gate, (_Float16*)out, pos,
                       1, (hipStream_t)stream, (const _Float16*)k, (const _Float16*)v));
   kv->len[layer] = pos + 1;
@@ -1059,7 +1015,7 @@ extern "C" mi_status mi_attn_verify(mi_kv* kv, int32_t layer, const mi_f16* q,
     return mi::fail(MI_ERR_OUT_OF_RANGE, "k = v = NULL but rows [%lld, %lld) are not in the "
                     "cache (len %lld)", (long long)past_pos, (long long)(past_pos + n),
                     (long long)kv->len[layer]);
-  if (past_pos + n > kv->cap) MI_TRY(mi_kv_reserve(kv, past_pos + n));
+  MI_TRY(mi::kv_grow(kv, past_pos + n, (hipStream_t)stream));
   MI_TRY(cache_attend(kv, layer, (const _Float16*)q, (const _Float16*)gate, (_Float16*)out,
                       past_pos, n, (hipStream_t)stream, (const _Float16*)k, (const _Float16*)v));
   kv->len[layer] = past_pos + n;
@@ -1114,7 +1070,7 @@ extern "C" mi_status mi_attn_step_proj(mi_kv* kv, int32_t layer, const float* q_
                     "rotary_dim=%d: the fused step rotates whole 64-column slices; use "
                     "mi_qk_norm_rope_append + mi_attn_decode",
                     rotary_dim);
-  if (pos + 1 > kv->cap) MI_TRY(mi_kv_reserve(kv, pos + 1));
+  MI_TRY(mi::kv_grow(kv, pos + 1, (hipStream_t)stream));
   ProjArgs x{};
   x.q_proj = q_proj;
   x.k = k;
@@ -1134,7 +1090,7 @@ extern "C" mi_status mi_attn_step_proj(mi_kv* kv, int32_t layer, const float* q_
   const int64_t rows = pos + 1;
   const SplitPlan plan = plan_split(rows, 1, kv->G, 1);
   void* ws;
-  MI_TRY(mi::kv_workspace(kv, split_workspace_bytes(1, kv->G, plan.max_chunks, 1), &ws));
+  MI_TRY(mi::kv_workspace(kv, split_workspace_bytes(1, kv->G, plan.max_chunks, 1), (hipStream_t)stream, &ws));
   AppendRows app;
   app.row0 = pos;
   app.n = 1;

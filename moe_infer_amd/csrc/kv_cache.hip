@@ -210,20 +210,40 @@ mi_status check_layer(const mi_kv* kv, int32_t layer) {
   return MI_OK;
 }
 
-mi_status kv_workspace(mi_kv* kv, size_t bytes, void** ws) {
+// Refuses an allocation on behalf of work enqueued on `stream` while that
+// stream is being captured into a graph: the captured kernels would hold
+// the address of memory the allocation replaces.
+mi_status no_capture(hipStream_t stream, const char* what) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  MI_HIP(hipStreamIsCapturing(stream, &cs));
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(MI_ERR_INVALID_ARG,
+                "%s needs to grow device memory while the stream is being captured; make one "
+                "eager call of the same or larger size first (mi_kv_reserve for the cache)",
+                what);
+  return MI_OK;
+}
+
+// A grown workspace replaces the old one, which is kept (not freed) until
+// mi_kv_destroy: graphs captured earlier hold its address and stay valid.
+mi_status kv_workspace(mi_kv* kv, size_t bytes, hipStream_t stream, void** ws) {
   if (bytes > kv->ws_bytes) {
-    if (kv->ws) {
-      MI_HIP(hipDeviceSynchronize());
-      (void)hipFree(kv->ws);
-      kv->ws = nullptr;
-      kv->ws_bytes = 0;
-    }
-    size_t b = bytes + bytes / 4;
-    MI_HIP(hipMalloc(&kv->ws, b));
+    MI_TRY(no_capture(stream, "the split-K workspace"));
+    void* p = nullptr;
+    const size_t b = bytes + bytes / 4;
+    MI_HIP(hipMalloc(&p, b));
+    if (kv->ws) kv->ws_retired.push_back(kv->ws);
+    kv->ws = p;
     kv->ws_bytes = b;
   }
   *ws = kv->ws;
   return MI_OK;
+}
+
+mi_status kv_grow(mi_kv* kv, int64_t rows, hipStream_t stream) {
+  if (rows <= kv->cap) return MI_OK;
+  MI_TRY(no_capture(stream, "the KV cache"));
+  return mi_kv_reserve(kv, rows);
 }
 
 mi_status kv_pack_rows(const _Float16* k, const _Float16* v, _Float16* dst_k, _Float16* dst_v,
@@ -276,6 +296,7 @@ extern "C" void mi_kv_destroy(mi_kv* kv) {
   (void)hipDeviceSynchronize();
   free_layers(kv);
   if (kv->ws) (void)hipFree(kv->ws);
+  for (void* p : kv->ws_retired) (void)hipFree(p);
   delete kv;
 }
 
@@ -357,7 +378,7 @@ extern "C" mi_status mi_kv_append(mi_kv* kv, int32_t layer, const mi_f16* k,
   if (!k || !v) return mi::fail(MI_ERR_INVALID_ARG, "null k/v");
   if (n <= 0) return mi::fail(MI_ERR_INVALID_ARG, "n=%d", n);
   if (pos < 0) return mi::fail(MI_ERR_OUT_OF_RANGE, "pos=%lld", (long long)pos);
-  if (pos + n > kv->cap) MI_TRY(mi_kv_reserve(kv, pos + n));
+  MI_TRY(mi::kv_grow(kv, pos + n, (hipStream_t)stream));
   MI_TRY(mi::kv_append_rows(kv, layer, (const _Float16*)k, (const _Float16*)v, pos, n,
                             (hipStream_t)stream));
   kv->len[layer] = pos + n;

@@ -1,0 +1,121 @@
+// Launch plans shared by the kernels, their host launchers and the CPU
+// model of their memory accesses (tests/copy_bounds_model.cc compiles this
+// header with g++): the causal prefill's per-wave tile schedule and the
+// split-K decode's chunking.  Plain C++ with no HIP dependency.
+#pragma once
+
+#include <cstdint>
+
+#if defined(__HIPCC__)
+#define MI_HD __host__ __device__
+#else
+#define MI_HD
+#endif
+
+namespace mi {
+
+// ------------------------------------------------------------- prefill --
+
+constexpr int kPrefillBQ = 128;  // queries per workgroup (4 waves of 32)
+constexpr int kPrefillBK = 64;   // keys per LDS tile
+
+// The key-tile range of one wave of the causal prefill: the wave owns
+// queries q0 + 32 w .. + 31 of query tile `qtile` (positions past + i), and
+// its workgroup walks key tiles 0 .. nt-1 (64 keys each) up to the last
+// key any of its queries sees.  Positions are 32-bit (the host checks
+// past + n + 2 * kPrefillBK < 2^31).
+struct PrefillWave {
+  int first;   // smallest query position of the wave
+  int last;    // largest query position of the wave (may be >= kv_len: padding)
+  int kv_len;  // rows in the cache after the append: past + n
+  int nt;      // key tiles the workgroup walks
+};
+
+MI_HD inline PrefillWave prefill_wave(int past, int n, int qtile, int w) {
+  PrefillWave p;
+  const int q0 = qtile * kPrefillBQ;
+  p.first = past + q0 + 32 * w;
+  p.last = p.first + 31;
+  p.kv_len = past + n;
+  const int end = past + q0 + kPrefillBQ < p.kv_len ? past + q0 + kPrefillBQ : p.kv_len;
+  p.nt = (end + kPrefillBK - 1) / kPrefillBK;
+  return p;
+}
+
+// Tile t of the wave's walk: does the wave attend it (some query sees a key
+// of it), is it on the wave's diagonal (needs the causal mask), and does it
+// take the steady-state schedule?  The steady schedule copies K(t+1) into
+// LDS unconditionally, so it is taken only when t + 1 < nt: a wave whose
+// queries all lie past n (padding of the last query tile) has its diagonal
+// beyond the last tile, so "not diagonal" alone would let it copy K(nt),
+// 64 rows past kv_len and possibly past the allocation.  Every other tile
+// copies K(t+1) only when t + 1 < nt, and V(t).
+MI_HD inline bool prefill_active(const PrefillWave& p, int t) {
+  return t * kPrefillBK <= p.last;
+}
+MI_HD inline bool prefill_diag(const PrefillWave& p, int t) {
+  return t * kPrefillBK + kPrefillBK - 1 > p.first;
+}
+MI_HD inline bool prefill_steady(const PrefillWave& p, int t, bool pending) {
+  return prefill_active(p, t) && pending && !prefill_diag(p, t) && t + 1 < p.nt;
+}
+
+// ----------------------------------------------------------- split-K --
+
+// Most chunks (partials) per sequence of one split launch.
+constexpr int kMaxSplitChunks = 1024;
+
+struct SplitKnobs {
+  int gh;     // KV heads per workgroup (2, or 1 when set to 1)
+  int wgs;    // target workgroup count
+  int chunk;  // fixed keys per chunk (0: planned)
+};
+
+struct SplitPlan {
+  int nwh, gh, ncb, chunk, max_chunks;
+};
+
+// Kernel variant and chunking of one split launch over sequences of at
+// most max_len rows.  Keys per chunk (per head): enough workgroups to
+// cover 256 CUs about once (K/V of one key and head is 1 KiB, so a 128-key
+// chunk of two heads moves 256 KiB and leaves one 8 KiB partial per head and
+// query token), at least one 32-key tile, at most 2048 keys (ragged batches
+// balance better with more workgroups), and at most kMaxSplitChunks chunks.
+// Chunks are whole 32-key tiles; the waves of a workgroup take its tiles
+// round-robin.  Decode rounds chunks to 32 keys: rounding up to 32 * NWH
+// would leave up to half the CUs idle just above a power of two (ctx 32769:
+// 129 workgroups instead of 256, 21.0 against 18.1 us per call).  The
+// 32-column verify (nq > 2) keeps whole wave rounds (measured ~1 us faster
+// at 65540 rows: 206 workgroups of 20 tiles against 242 of 17).
+inline SplitPlan plan_split(int64_t max_len, int64_t batch, int G, int nq, const SplitKnobs& k) {
+  SplitPlan p;
+  p.ncb = nq <= 2 ? 1 : 2;
+  if (p.ncb == 2) {  // 32 columns: 4 waves, one head (registers and LDS)
+    p.nwh = 4;
+    p.gh = 1;
+  } else if (G % 2 == 0 && k.gh == 2) {
+    p.nwh = 4;
+    p.gh = 2;
+  } else {
+    p.nwh = 8;
+    p.gh = 1;
+  }
+  const int64_t step = 32 * p.nwh;
+  const int64_t target_wgs = k.wgs > 0 ? k.wgs : 1;
+  int64_t chunk = k.chunk;
+  if (chunk <= 0) {
+    chunk = (batch * G * max_len + p.gh * target_wgs - 1) / (p.gh * target_wgs);
+    if (chunk > 2048) chunk = 2048;
+  }
+  const int64_t min_chunk = (max_len + kMaxSplitChunks - 1) / kMaxSplitChunks;
+  if (chunk < min_chunk) chunk = min_chunk;
+  const int64_t gran = p.ncb == 2 ? step : 32;
+  chunk = (chunk + gran - 1) / gran * gran;
+  if (chunk < gran) chunk = gran;  // also for max_len == 0
+  p.chunk = (int)chunk;
+  p.max_chunks = (int)((max_len + chunk - 1) / chunk);
+  if (p.max_chunks < 1) p.max_chunks = 1;
+  return p;
+}
+
+}  // namespace mi

@@ -21,12 +21,13 @@
 //    order is chosen so that P^T is the lane's own S^T accumulator.
 //  * Epilogue: divide by the row sum, multiply by sigmoid(gate), write f16.
 #include "common.h"
+#include "plan.h"
 
 namespace {
 
 constexpr int D = mi::kHeadDim;
-constexpr int BQ = 128;        // queries per workgroup
-constexpr int BK = 64;         // keys per LDS tile
+constexpr int BQ = mi::kPrefillBQ;  // queries per workgroup
+constexpr int BK = mi::kPrefillBK;  // keys per LDS tile
 // K tile in LDS: two 32-key blocks copied verbatim from the cache layout
 // (mi::k_offset), unpadded.  An A-operand read then hits each LDS bank once
 // per 16-byte slot (rocprofv3 SQ_LDS_BANK_CONFLICT: 0); with the two row
@@ -110,12 +111,10 @@ attn_prefill_kernel(PrefillArgs a) {
   }
   // In-kernel positions are 32-bit (the host checks past + n < 2^31).
   const int past = (int)a.past;
-  const int qpos = past + qi;                  // this lane's query position
-  const int wave_first = past + q0 + 32 * w;   // smallest query position of the wave
-  const int wave_last = wave_first + 31;
-  const int kv_len = past + a.n;
-  const int kv_end = min(past + q0 + BQ, kv_len);
-  const int nt = (kv_end + BK - 1) / BK;
+  const int qpos = past + qi;  // this lane's query position
+  const mi::PrefillWave pw = mi::prefill_wave(past, a.n, qtile, w);
+  const int kv_len = pw.kv_len;
+  const int nt = pw.nt;
   const float c2 = a.scale_log2e;
 
   f32x16 acc[8];
@@ -402,15 +401,13 @@ attn_prefill_kernel(PrefillArgs a) {
   };
   for (int t = 0; t < nt; t++) {
     const int key0 = t * BK;
-    const bool active = key0 <= wave_last;
-    const bool diag = key0 + BK - 1 > wave_first;
+    const bool active = mi::prefill_active(pw, t);
+    const bool diag = mi::prefill_diag(pw, t);
     float alpha = 1.f;
     f32x16 st[2];
     // Steady state: not the wave's first or diagonal tile, and not the last
-    // tile (the steady schedule copies K(t+1)).  A wave whose queries are all
-    // past n has its diagonal beyond the last tile, so `!diag` alone does not
-    // imply t + 1 < nt: K(nt) can lie past the end of the allocation.
-    if (active && pending && !diag && t + 1 < nt) {
+    // tile (the steady schedule copies K(t+1); mi::prefill_steady).
+    if (mi::prefill_steady(pw, t, pending)) {
       steady(t, alpha);
     } else {
       if (t + 1 < nt) load_k(t + 1);

@@ -141,7 +141,7 @@ extern "C" mi_status mi_qk_norm_rope_append(mi_kv* kv, int32_t layer, const floa
   if (n <= 0) return mi::fail(MI_ERR_INVALID_ARG, "n=%d", n);
   if (pos < 0) return mi::fail(MI_ERR_OUT_OF_RANGE, "pos=%lld", (long long)pos);
   MI_TRY(mi::check_rope(kv, rotary_dim, rope_theta, eps));
-  if (pos + n > kv->cap) MI_TRY(mi_kv_reserve(kv, pos + n));
+  MI_TRY(mi::kv_grow(kv, pos + n, (hipStream_t)stream));
 
   RopeArgs a{};
   a.q_proj = q_proj;

@@ -44,6 +44,20 @@ def record_engine_telemetry(on: bool) -> None:
     _RECORD_TELEMETRY = bool(on)
 
 
+class EngineInterrupted(RuntimeError):
+    """Raised when a forward call's check_signal returns True before a layer
+    (the reference's MoEError::Metal("interrupted"), surfaced to Python as a
+    RuntimeError: fused_exp2.rs:1017-1019, python_bindings.rs:152)."""
+
+    def __init__(self):
+        super().__init__("Metal error: interrupted")
+
+
+def _poll(check_signal) -> None:
+    if check_signal is not None and check_signal():
+        raise EngineInterrupted()
+
+
 @dataclass(frozen=True)
 class EngineSnapshot:
     pos: int
@@ -99,25 +113,35 @@ class Engine:
             self._telemetry.setdefault(key, []).append((time.perf_counter() - t0) * 1e3)
 
     # -- main model ------------------------------------------------------------
-    def forward(self, layers):
+    def forward(self, layers, check_signal=None):
         """layers: sequence of (layer, q[H*D], k[G*D], v[G*D], gate|None).
-        Returns the gated attention outputs, one per entry."""
+        Returns the gated attention outputs, one per entry.
+
+        check_signal: optional callable polled before every layer; when it
+        returns True the call raises EngineInterrupted and engine_pos is not
+        advanced (rows already appended by earlier layers stay past len and
+        are overwritten by the next call at the same position), as the
+        reference's per-layer poll does (fused_exp2.rs:1017-1019)."""
         t0 = time.perf_counter()
         pos = self.cache.pos
-        outs = [attention.attn_step(self.cache, layer, q, k, v, pos, gate=gate)
-                for layer, q, k, v, gate in layers]
+        outs = []
+        for layer, q, k, v, gate in layers:
+            _poll(check_signal)
+            outs.append(attention.attn_step(self.cache, layer, q, k, v, pos, gate=gate))
         self.cache.set_pos(pos + 1)
         self.cache.gpu_dirty = True
         self._record("engine.full_attention_ms", t0)
         return outs
 
-    def forward_batched(self, layers):
+    def forward_batched(self, layers, check_signal=None):
         """layers: sequence of (layer, q[n,H,D], k[n,G*D], v[n,G*D], gate|None);
-        n == 1 falls back to the token-serial step (fused_exp3.rs:169-171)."""
+        n == 1 falls back to the token-serial step (fused_exp3.rs:169-171).
+        check_signal: as for forward()."""
         t0 = time.perf_counter()
         pos = self.cache.pos
         outs, n = [], None
         for layer, q, k, v, gate in layers:
+            _poll(check_signal)
             n_l = q.numel() // (self.cache.num_q_heads * self.cache.head_dim)
             if n is not None and n_l != n:
                 raise ValueError("every layer must carry the same token count")
@@ -135,30 +159,36 @@ class Engine:
         return outs
 
     # -- the same steps from the projections -------------------------------------
-    def forward_proj(self, layers):
+    def forward_proj(self, layers, check_signal=None):
         """layers: sequence of (layer, q_proj[H,2D] f32, k[G,D] f32, v[G,D] f32,
         q_norm_w[D] bf16, k_norm_w[D] bf16).  Norm + RoPE at engine_pos, append,
-        attend [0, pos], gate from q_proj; then pos += 1."""
+        attend [0, pos], gate from q_proj; then pos += 1.  check_signal: as for
+        forward()."""
         t0 = time.perf_counter()
         pos = self.cache.pos
-        outs = [attention.attn_step_proj(self.cache, layer, qp, k, v, qw, kw, pos,
-                                         rotary_dim=self.rotary_dim, rope_theta=self.rope_theta,
-                                         eps=self.rms_norm_eps)
-                for layer, qp, k, v, qw, kw in layers]
+        outs = []
+        for layer, qp, k, v, qw, kw in layers:
+            _poll(check_signal)
+            outs.append(attention.attn_step_proj(self.cache, layer, qp, k, v, qw, kw, pos,
+                                                 rotary_dim=self.rotary_dim,
+                                                 rope_theta=self.rope_theta,
+                                                 eps=self.rms_norm_eps))
         self.cache.set_pos(pos + 1)
         self.cache.gpu_dirty = True
         self._record("engine.full_attention_ms", t0)
         return outs
 
-    def forward_batched_proj(self, layers):
+    def forward_batched_proj(self, layers, check_signal=None):
         """layers: sequence of (layer, q_proj[n,H,2D], k[n,G,D], v[n,G,D],
         q_norm_w, k_norm_w), all f32 but the bf16 weights; token i at
-        position engine_pos + i.  Returns [n,H,D] f16 per layer; pos += n."""
+        position engine_pos + i.  Returns [n,H,D] f16 per layer; pos += n.
+        check_signal: as for forward()."""
         t0 = time.perf_counter()
         pos = self.cache.pos
         outs, n = [], None
         H, D = self.cache.num_q_heads, self.cache.head_dim
         for layer, qp, k, v, qw, kw in layers:
+            _poll(check_signal)
             n_l = qp.numel() // (H * 2 * D)
             if n is not None and n_l != n:
                 raise ValueError("every layer must carry the same token count")

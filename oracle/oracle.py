@@ -300,3 +300,35 @@ class CacheModel:
         self.v = [a.copy() for a in other.v]
         self.len = list(other.len)
         self.pos = other.pos
+
+
+# ------------------------------------------------ CPU baseline (bench.py) --
+
+class DecodeBaseline:
+    """The reference CPU engine's attention core for one decode step, as
+    cpu.rs:146-167 runs it: scores -> softmax -> values -> sigmoid gate over
+    an f32 cache, with the scores buffer allocated once at the cache's
+    max_seq (the engine's scratch, cpu.rs:149-163).  The f16 inputs are
+    widened to f32 once, here, so that run() times only the reference's f32
+    loops (src/math_util.rs:264-269, 323-383)."""
+
+    def __init__(self, q, k_rows, v_rows, gate, H=16, G=2, D=256):
+        self.H, self.G, self.D = H, G, D
+        self.q = f16_to_f32(_h(q).view(np.uint16))
+        self.gate = f16_to_f32(_h(gate).view(np.uint16))
+        self.k = f16_to_f32(_h(k_rows).view(np.uint16))
+        self.v = f16_to_f32(_h(v_rows).view(np.uint16))
+        self.max_seq = self.k.size // (G * D)
+        self.scores = np.zeros(H * self.max_seq, dtype=np.float32)
+        self.out = np.empty(H * D, dtype=np.float32)
+        self._args = [_p(a) for a in (self.q, self.gate, self.k, self.v, self.scores, self.out)]
+
+    def run(self, seq_len: int) -> np.ndarray:
+        L = lib()
+        q, gate, k, v, scores, out = self._args
+        H, G, D = self.H, self.G, self.D
+        L.oracle_attention_scores_batched(q, k, scores, H, G, D, G * D, seq_len, self.max_seq)
+        L.oracle_attention_softmax_batched(scores, H, seq_len, self.max_seq)
+        L.oracle_attention_values_batched(scores, v, out, H, G, D, G * D, seq_len, self.max_seq)
+        L.oracle_sigmoid_gate_inplace(out, gate, H * D)
+        return self.out.reshape(H, D)

@@ -1,0 +1,113 @@
+// CPU model of the rows the attention kernels read, over the launch plans of
+// moe_infer_amd/csrc/plan.h (the same header the kernels and their launchers
+// use).  Built and run by tests/test_copy_bounds.py; prints one line per
+// check: "<name> <cases> <violations>".
+//
+// Prefill (attn_prefill_kernel): every wave copies K tile 0 before its loop;
+// at tile t the steady schedule (mi::prefill_steady) copies K(t+1) and V(t),
+// any other tile copies K(t+1) when t + 1 < nt, and V(t).  A tile is rows
+// [64 T, 64 T + 64) of both K and V; the cache holds round_cap(past + n) rows
+// at least (capacities are multiples of 256 rows).  The same walk with the
+// steady condition lacking "t + 1 < nt" is checked too, and must find
+// violations: it is the copy past the allocation that faulted before the
+// condition was added.
+//
+// Split-K decode / verify (attn_split_kernel, non-ragged): chunk c covers
+// keys [c * chunk, min((c+1) * chunk, len)); wave w of NWH reads whole
+// 32-key tiles k0 = begin + 32 w + 32 NWH i while k0 < end.  Each tile must
+// be 32-aligned and lie inside round_cap(len) rows, chunks must number at
+// most kMaxSplitChunks (the combine kernel merges at most that many).
+#include <cstdio>
+#include <initializer_list>
+
+#include "plan.h"
+
+static long long round_cap(long long rows) {
+  if (rows < 256) rows = 256;
+  return (rows + 255) / 256 * 256;
+}
+
+// Walks one (past, n) prefill; returns the number of tile copies that leave
+// `cap` rows.  old_rule: the steady condition without "t + 1 < nt".
+static long long prefill_violations(int past, int n, long long cap, bool old_rule) {
+  long long bad = 0;
+  auto copy = [&](int T) {
+    if ((long long)T * mi::kPrefillBK + mi::kPrefillBK > cap) bad++;
+  };
+  const int ntiles = (n + mi::kPrefillBQ - 1) / mi::kPrefillBQ;
+  for (int qt = 0; qt < ntiles; qt++)
+    for (int w = 0; w < 4; w++) {
+      const mi::PrefillWave p = mi::prefill_wave(past, n, qt, w);
+      copy(0);
+      bool pending = false;
+      for (int t = 0; t < p.nt; t++) {
+        const bool active = mi::prefill_active(p, t);
+        bool steady = mi::prefill_steady(p, t, pending);
+        if (old_rule) steady = active && pending && !mi::prefill_diag(p, t);
+        if (steady) {
+          copy(t + 1);
+        } else if (t + 1 < p.nt) {
+          copy(t + 1);
+        }
+        copy(t);  // V(t)
+        pending = active;
+      }
+    }
+  return bad;
+}
+
+// Tiles of one split launch over `len` rows with `nq` query tokens.
+static long long split_violations(long long len, int nq, const mi::SplitKnobs& k) {
+  const mi::SplitPlan p = mi::plan_split(len, 1, 2, nq, k);
+  long long bad = 0;
+  if (p.max_chunks > mi::kMaxSplitChunks || p.chunk % 32) bad++;
+  const long long cap = round_cap(len);
+  for (long long c = 0; c < p.max_chunks; c++) {
+    const long long b = c * p.chunk;
+    if (b >= len) continue;
+    const long long e = b + p.chunk < len ? b + p.chunk : len;
+    for (int w = 0; w < p.nwh; w++)
+      for (long long k0 = b + 32 * w; k0 < e; k0 += 32LL * p.nwh)
+        if (k0 % 32 || k0 + 32 > cap) bad++;
+  }
+  if ((long long)p.max_chunks * p.chunk < len) bad++;  // every key covered
+  return bad;
+}
+
+int main() {
+  long long cases = 0, bad_new = 0, bad_old = 0;
+  for (int past = 0; past < 700; past++)
+    for (int n = 1; n < 700; n++) {
+      const long long cap = round_cap((long long)past + n);
+      bad_new += prefill_violations(past, n, cap, false);
+      bad_old += prefill_violations(past, n, cap, true);
+      cases++;
+    }
+  std::printf("prefill %lld %lld\n", cases, bad_new);
+  std::printf("prefill_without_last_tile_rule %lld %lld\n", cases, bad_old);
+  // long pasts and C4-adjacent sizes
+  long long c2 = 0, b2 = 0;
+  for (int past : {0, 32768, 65000, 65535, 131071})
+    for (int n : {1, 127, 128, 129, 257, 1000, 4095, 4096, 4097}) {
+      b2 += prefill_violations(past, n, round_cap((long long)past + n), false);
+      c2++;
+    }
+  std::printf("prefill_long %lld %lld\n", c2, b2);
+
+  const mi::SplitKnobs knobs[] = {{2, 256, 0}, {1, 256, 0}, {2, 1000, 0}, {2, 7, 0}, {2, 256, 100}};
+  long long cs = 0, bs = 0;
+  for (const auto& k : knobs)
+    for (int nq = 1; nq <= 4; nq++) {
+      for (long long len = 1; len <= 5000; len++) {
+        bs += split_violations(len, nq, k);
+        cs++;
+      }
+      for (long long len : {32767LL, 32768LL, 32769LL, 65536LL, 65540LL, 262144LL, 262161LL,
+                            1000000LL, 2097152LL, 4194304LL}) {
+        bs += split_violations(len, nq, k);
+        cs++;
+      }
+    }
+  std::printf("split %lld %lld\n", cs, bs);
+  return 0;
+}

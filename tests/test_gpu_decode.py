@@ -1,6 +1,8 @@
 """Decode, engine step and K-token verify on the GPU against the CPU oracle
 (reference f32 math of src/math_util.rs:264-269, 323-383 on the same f16
 inputs), through the C ABI."""
+import warnings
+
 import numpy as np
 import pytest
 import torch
@@ -226,6 +228,51 @@ def test_graph_replay_of_steps_matches_eager():
             assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"replay {r}"
     assert_close(out1, O.decode(host(q), k[:L + 1], v[:L + 1], L + 1, gate=host(g)),
                  "graph step vs oracle")
+
+
+def test_graph_survives_workspace_growth_on_the_same_handle():
+    """A graph captured at a short context keeps replaying correctly after an
+    eager call on the same handle grows its split-K workspace (the old
+    workspace is kept, not freed); a call that would grow the workspace or
+    the cache while the stream is capturing is refused with a ValueError."""
+    from moe_infer_amd import _lib
+    announce("graph + workspace growth on one handle")
+    rng = np.random.default_rng(32)
+    L, LONG = 3000, 200_000
+    k, v = f16(rng, L + 1, G * D), f16(rng, L + 1, G * D)
+    c = filled_cache(k[:L], v[:L], capacity=LONG)
+    q, g = dev(f16(rng, H * D)), dev(f16(rng, H * D))
+    kn, vn = dev(k[L]), dev(v[L])
+    out = torch.empty(H * D, dtype=torch.float16, device="cuda")
+    attn_step(c, 0, q, kn, vn, L, gate=g, out=out)  # sizes the workspace for L
+    torch.cuda.synchronize()
+    ref = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        attn_step(c, 0, q, kn, vn, L, gate=g, out=out)
+    # growth refused under capture: the workspace (a long decode) and the cache
+    refused = []
+    g2 = torch.cuda.CUDAGraph()
+    with warnings.catch_warnings(), torch.cuda.graph(g2):  # captures nothing: both refused
+        warnings.simplefilter("ignore", UserWarning)
+        for fn in (lambda: attn_decode(c, 0, q, LONG, out=torch.empty_like(out)),
+                   lambda: attn_step(c, 0, q, kn, vn, 2 * LONG, out=torch.empty_like(out))):
+            try:
+                fn()
+            except _lib.MiValueError as e:
+                refused.append(str(e))
+    del g2
+    assert len(refused) == 2 and all("captur" in m for m in refused), refused
+    # an eager long decode grows the workspace; the earlier graph still replays
+    long_out = attn_decode(c, 0, q, LONG)
+    torch.cuda.synchronize()
+    assert torch.isfinite(long_out.float()).all()
+    for r in range(3):
+        out.fill_(7.0)
+        graph.replay()
+        attn_decode(c, 0, q, LONG, out=long_out)  # eager work on the grown workspace
+        torch.cuda.synchronize()
+        assert torch.equal(ref.view(torch.int16), out.view(torch.int16)), f"replay {r}"
 
 
 def test_gate_extremes_decode_and_prefill():

@@ -99,3 +99,39 @@ def test_prefill_cache_full_to_capacity(past, n):
     out = attn_prefill(c, 0, dev(q), dev(k), dev(v), past)
     ref = O.causal(q, np.concatenate([kp, k]), np.concatenate([vp, v]), past)
     assert_close(out, ref, f"prefill full cache past={past} n={n}")
+
+
+@pytest.mark.parametrize("past,n", [(32768, 257), (32768, 1000), (65000, 257), (65000, 1000),
+                                    (0, 4095), (0, 4097)])
+def test_prefill_long_past_and_c4_adjacent(past, n):
+    """Chunked prefill after a long prompt (the engine's forward_batched with
+    n > 16 at a large engine_pos, src/engine/qwen35_moe/batched.rs:233-260)
+    and the sizes either side of C4: sampled rows against the oracle, and
+    every row equal to a GPU decode of the same query at seq_len
+    past + i + 1."""
+    import torch
+    from moe_infer_amd import kv_cache_append
+    announce(f"prefill long past={past} n={n}")
+    rng = np.random.default_rng(past + n)
+    gen = torch.Generator(device="cuda").manual_seed(past + 7 * n)
+    c = Cache(num_layers=1, capacity=past + n)
+    if past:
+        kp = torch.randn(past, G * D, generator=gen, device="cuda").half()
+        vp = torch.randn(past, G * D, generator=gen, device="cuda").half()
+        kv_cache_append(c, 0, kp, vp, 0)
+        c.set_pos(past)
+    q, k, v, g = f16(rng, n, H, D), f16(rng, n, G * D), f16(rng, n, G * D), f16(rng, n, H, D)
+    qd, gd = dev(q), dev(g)
+    out = host(attn_prefill(c, 0, qd, dev(k), dev(v), past, gate=gd))
+    assert np.all(np.isfinite(out))
+    kall, vall = c.download(0, rows=past + n)
+    assert np.array_equal(kall[past:].view(np.uint16), k.view(np.uint16))
+    assert np.array_equal(vall[past:].view(np.uint16), v.view(np.uint16))
+    for i in sorted({0, 1, 63, 64, 127, 128, n // 2, n - 2, n - 1}):
+        ref = O.decode(q[i].ravel(), kall, vall, past + i + 1, gate=g[i].ravel())
+        assert_close(out[i], ref, f"prefill past={past} n={n} row {i}")
+    dec = torch.empty(n, H, D, dtype=torch.float16, device="cuda")
+    for i in range(n):
+        attn_decode(c, 0, qd[i], past + i + 1, gate=gd[i], out=dec[i])
+    assert_close(out, host(dec), f"prefill past={past} n={n}: all rows vs GPU decode",
+                 atol=1e-3)
