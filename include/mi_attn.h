@@ -218,6 +218,30 @@ mi_status mi_attn_decode_ragged(const mi_f16* k_rows, const mi_f16* v_rows,
                                 void* workspace, size_t workspace_bytes,
                                 mi_stream stream);
 
+/* Bytes of the device-resident scratch array behind
+ * mi_attn_decode_ragged_noalloc (one copy per device, held until the process
+ * ends): 16 MiB, which covers batches up to ~760 sequences at the Qwen3.6
+ * shape (16 query / 2 KV heads, head_dim 256). */
+#define MI_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* mi_attn_decode_ragged without a workspace argument, for callers that
+ * cannot allocate device memory (code under graph capture, serving loops
+ * and harnesses that forbid hipMalloc): the workspace is a file-scope
+ * device array of MI_NOALLOC_SCRATCH_BYTES.  The call allocates and frees
+ * nothing; a batch whose mi_attn_ragged_workspace_size exceeds the array
+ * returns MI_ERR_UNSUPPORTED.  Every call on one device shares that
+ * device's array: calls that overlap in time on one device (other streams
+ * or threads) race on it and must be serialised by the caller.  Same
+ * arguments and results as mi_attn_decode_ragged otherwise.
+ * No counterpart in the reference (whose decode is single-sequence). */
+mi_status mi_attn_decode_ragged_noalloc(const mi_f16* k_rows, const mi_f16* v_rows,
+                                        const int32_t* offsets, const int32_t* lengths,
+                                        int32_t batch, int32_t max_len,
+                                        int32_t num_q_heads, int32_t num_kv_heads,
+                                        int32_t head_dim, const mi_f16* q,
+                                        const mi_f16* gate, mi_f16* out,
+                                        mi_stream stream);
+
 /* Layout helper for callers that build ragged buffers themselves: writes
  * `rows` token-major rows k_rows, v_rows ([rows][G*D]) at rows
  * [row0, row0+rows) of dst_k / dst_v in the device layout above (rows of

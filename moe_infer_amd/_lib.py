@@ -56,6 +56,7 @@ SIGNATURES = [
     ("mi_attn_verify", ST, [P, I32, P, P, P, P, P, I64, I32, P]),
     ("mi_attn_ragged_workspace_size", SZ, [I32, I32, I32, I32, I32]),
     ("mi_attn_decode_ragged", ST, [P, P, P, P, I32, I32, I32, I32, I32, P, P, P, P, SZ, P]),
+    ("mi_attn_decode_ragged_noalloc", ST, [P, P, P, P, I32, I32, I32, I32, I32, P, P, P, P]),
     ("mi_kv_pack", ST, [P, P, P, P, I64, I64, I32, I32, P]),
     ("mi_qk_norm_rope_append", ST, [P, I32, P, P, P, P, P, I32, C.c_float, C.c_float, I64, I32,
                                     P, P, P]),

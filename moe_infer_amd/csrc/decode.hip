@@ -1100,3 +1100,57 @@ extern "C" mi_status mi_attn_step_proj(mi_kv* kv, int32_t layer, const float* q_
   kv->len[layer] = pos + 1;
   return MI_OK;
 }
+
+// ------------------------------------------- allocation-free ragged decode --
+//
+// The ragged decode's workspace (split partials + tile offsets) as a
+// file-scope device array, for callers that cannot allocate.  Each device
+// the library runs on holds its own copy until the process ends; host code
+// reaches it only through the address hipGetSymbolAddress returns for the
+// current device (the array's name in host code is not a device address).
+// Nothing in it has to start at zero: the plan kernel writes every tile
+// offset and the split kernel writes every partial slot the merge reads.
+static __device__ __align__(256) unsigned char scratch[MI_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// The current device's copy of `scratch`, looked up once per device.
+mi_status scratch_ptr(void** out) {
+  int dev = 0;
+  MI_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices)
+    return mi::fail(MI_ERR_UNSUPPORTED, "device %d beyond the %d the library tracks", dev,
+                    kMaxDevices);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    MI_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return MI_OK;
+}
+}  // namespace
+
+extern "C" mi_status mi_attn_decode_ragged_noalloc(
+    const mi_f16* k_rows, const mi_f16* v_rows, const int32_t* offsets, const int32_t* lengths,
+    int32_t batch, int32_t max_len, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, const mi_f16* q, const mi_f16* gate, mi_f16* out, mi_stream stream) {
+  mi::clear_error();
+  MI_TRY(mi::check_shape(num_q_heads, num_kv_heads, head_dim));
+  if (batch <= 0 || max_len < 0)
+    return mi::fail(MI_ERR_INVALID_ARG, "batch=%d max_len=%d", batch, max_len);
+  const size_t need =
+      mi_attn_ragged_workspace_size(batch, max_len, num_q_heads, num_kv_heads, head_dim);
+  if (need > (size_t)MI_NOALLOC_SCRATCH_BYTES)
+    return mi::fail(MI_ERR_UNSUPPORTED,
+                    "batch=%d needs %zu bytes of scratch; the static scratch holds %zu "
+                    "(use mi_attn_decode_ragged with a workspace)",
+                    batch, need, (size_t)MI_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  MI_TRY(scratch_ptr(&ws));
+  return mi_attn_decode_ragged(k_rows, v_rows, offsets, lengths, batch, max_len, num_q_heads,
+                               num_kv_heads, head_dim, q, gate, out, ws,
+                               (size_t)MI_NOALLOC_SCRATCH_BYTES, stream);
+}
