@@ -778,11 +778,13 @@ int env_int(const char* name, int dflt) {
 }
 
 // Split-planning knobs, read once per process (measurement aids; the
-// defaults are the tuned values): MI_ATTN_SPLIT_GH=1 puts one KV head per
-// workgroup, MI_ATTN_SPLIT_WGS sets the target workgroup count,
+// defaults are the tuned values): MI_ATTN_SPLIT_GH=2 puts both KV heads of
+// a Qwen3.6 layer in one workgroup (default one head per workgroup: at C2
+// the same split time with half the partials, 18.8 against 19.5 us per
+// step), MI_ATTN_SPLIT_WGS sets the target workgroup count,
 // MI_ATTN_SPLIT_CHUNK fixes the keys per chunk.
 const mi::SplitKnobs& split_knobs() {
-  static const mi::SplitKnobs k{env_int("MI_ATTN_SPLIT_GH", 2),
+  static const mi::SplitKnobs k{env_int("MI_ATTN_SPLIT_GH", 1),
                                 std::max(1, env_int("MI_ATTN_SPLIT_WGS", 256)),
                                 std::max(0, env_int("MI_ATTN_SPLIT_CHUNK", 0))};
   return k;
