@@ -465,7 +465,11 @@ def main():
         line["roofline"] = {"bound": "hbm", "kernel": "attn_split_kernel (decode, C2)",
                             "achieved": round(ach, 1), "peak": hbm_peak, "unit": "GB/s",
                             "frac": round(ach / hbm_peak, 4),
-                            "traffic": traffic_of("decode_split_c2")}
+                            "traffic": traffic_of("decode_split_c2"),
+                            # the whole call (append + split + combine, launch gaps
+                            # included): algorithmic bytes / step time per layer
+                            "whole_call_achieved": round(d["gbps"], 1),
+                            "whole_call_frac": round(d["gbps"] / hbm_peak, 4)}
         line["decode"] = {k2: (round(v2, 3) if isinstance(v2, float) else v2)
                           for k2, v2 in d.items()}
     if p:
@@ -477,6 +481,15 @@ def main():
                                     "traffic": traffic_of("prefill_c4")}
         line["prefill"] = {k2: (round(v2, 3) if isinstance(v2, float) else v2)
                            for k2, v2 in p.items()}
+    vr = rec.get("verify")
+    if vr:
+        ach = C5_BYTES / (vr["split_kernel_us"] * 1e3)
+        line["roofline_verify"] = {"bound": "hbm", "kernel": "attn_split_kernel (verify, C5)",
+                                   "achieved": round(ach, 1), "peak": hbm_peak, "unit": "GB/s",
+                                   "frac": round(ach / hbm_peak, 4),
+                                   "traffic": traffic_of("verify_split_c5"),
+                                   "whole_call_achieved": round(vr["gbps"], 1),
+                                   "whole_call_frac": round(vr["gbps"] / hbm_peak, 4)}
     for key in ("verify", "ragged", "oproj"):
         if key in rec:
             line[key] = {k2: (round(v2, 3) if isinstance(v2, float) else v2)

@@ -214,7 +214,7 @@ attn_split_kernel(SplitArgs a, X x) {
   constexpr bool kProj = is_proj<X>::value;
   extern __shared__ float smem[];
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int hw = wv / NWH;   // KV head of this wave within the workgroup
   const int w = wv % NWH;    // wave within the head
   const int g = lane >> 4;   // lane group: k-slot group of the MFMA operands
