@@ -164,6 +164,11 @@ class Cache:
 
     # -- persistence --------------------------------------------------------
     def save(self, bin_path: str, json_path: str) -> None:
+        """Writes the reference's manifest layout (cache.rs:133-175) with f16
+        K/V and only the full-attention layers.  Files saved here load here
+        (and the reference's float32 files load here too); the reference's
+        Cache::load reads every tensor as float32 over its full layer list,
+        so it cannot read these."""
         if self.gpu_dirty:
             import sys
             print("[cache] WARNING: saving cache with gpu_dirty=true", file=sys.stderr)
