@@ -1118,10 +1118,17 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::atomic<void*> g_scratch_ptr[kMaxDevices];
 
-// The current device's copy of `scratch`, looked up once per device.
-mi_status scratch_ptr(void** out) {
+// The current device's copy of `scratch`, looked up once per device.  The
+// launch stream must belong to the current device: the copy is per device.
+mi_status scratch_ptr(hipStream_t stream, void** out) {
   int dev = 0;
   MI_HIP(hipGetDevice(&dev));
+  if (stream) {
+    int sdev = 0;
+    MI_HIP(hipStreamGetDevice(stream, &sdev));
+    if (sdev != dev)
+      return mi::fail(MI_ERR_INVALID_ARG, "stream on device %d, current device %d", sdev, dev);
+  }
   if (dev < 0 || dev >= kMaxDevices)
     return mi::fail(MI_ERR_UNSUPPORTED, "device %d beyond the %d the library tracks", dev,
                     kMaxDevices);
@@ -1151,7 +1158,7 @@ extern "C" mi_status mi_attn_decode_ragged_noalloc(
                     "(use mi_attn_decode_ragged with a workspace)",
                     batch, need, (size_t)MI_NOALLOC_SCRATCH_BYTES);
   void* ws = nullptr;
-  MI_TRY(scratch_ptr(&ws));
+  MI_TRY(scratch_ptr((hipStream_t)stream, &ws));
   return mi_attn_decode_ragged(k_rows, v_rows, offsets, lengths, batch, max_len, num_q_heads,
                                num_kv_heads, head_dim, q, gate, out, ws,
                                (size_t)MI_NOALLOC_SCRATCH_BYTES, stream);
