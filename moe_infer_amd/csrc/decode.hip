@@ -584,26 +584,30 @@ struct CombineArgs {
   int64_t nslots;           // partial slots per KV head (SplitArgs::nslots)
 };
 
-// Chunk merge.  One workgroup per (column, KV head x 16-column slice,
-// sequence), 256 threads.  Every global load is issued up front: each
+// Chunk merge.  One workgroup per (column, KV head x slice of S values of
+// d, sequence), 256 threads.  Every global load is issued up front: each
 // thread's (m_c, l_c) for chunks t, t+256, ... and its partial outputs o_c[d]
-// (column d0 + t%16, chunks congruent to t/16 mod 16, up to kBatch of
-// them).  The max and the sum over chunks are wave reductions in DPP
-// followed by one LDS exchange each.
+// (d = d0 + t%S, chunks congruent to t/S mod 256/S, up to kBatch of them).
+// The max and the sum over chunks are wave reductions in DPP followed by one
+// LDS exchange each.
 // out = sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M), zero when the
 // denominator is zero (the reference's `sum > 0` guard and zero-filled
 // output, math_util.rs:357, 372), then * sigmoid(gate).
-constexpr int kCombineSlice = 16;
 constexpr int kMaxChunks = mi::kMaxSplitChunks;
 
 extern "C" __device__ float __ockl_wfred_max_f32(float);
 extern "C" __device__ float __ockl_wfred_add_f32(float);
 
+// S = kCombineSlice values of d per workgroup: 16 for up to 16 columns
+// (decode), 32 for the 32-column verify (measured: decode step 18.9 / 19.2 /
+// 19.3 us with S = 16 / 32 / 8, verify 33.1 / 32.7 / 34.6 us).
+template <int kCombineSlice>
 __global__ void __launch_bounds__(256)
 attn_combine_kernel(CombineArgs a) {
+  constexpr int kCombineGroups = 256 / kCombineSlice;  // chunk groups of a workgroup
   __shared__ float red[2][4];
   __shared__ float wts[kMaxChunks];
-  __shared__ float acc_s[16][kCombineSlice + 1];
+  __shared__ float acc_s[kCombineGroups][kCombineSlice + 1];
   const int c = blockIdx.x;
   const int kvh = blockIdx.y / (D / kCombineSlice);
   const int d0 = (blockIdx.y % (D / kCombineSlice)) * kCombineSlice;
@@ -638,7 +642,7 @@ attn_combine_kernel(CombineArgs a) {
   float ov[kBatch];
 #pragma unroll
   for (int u = 0; u < kBatch; u++) {
-    const int ch = cg + 16 * u;
+    const int ch = cg + kCombineGroups * u;
     ov[u] = ch < nch ? po[ch * ostride] : 0.f;
   }
   float mx = kNegBig;
@@ -665,16 +669,17 @@ attn_combine_kernel(CombineArgs a) {
   float o = 0.f;
 #pragma unroll
   for (int u = 0; u < kBatch; u++) {
-    const int ch = cg + 16 * u;
+    const int ch = cg + kCombineGroups * u;
     if (ch < nch) o += ov[u] * wts[ch];
   }
-  for (int ch = cg + 16 * kBatch; ch < nch; ch += 16) o += po[ch * ostride] * wts[ch];
+  for (int ch = cg + kCombineGroups * kBatch; ch < nch; ch += kCombineGroups)
+    o += po[ch * ostride] * wts[ch];
   acc_s[cg][dl] = o;
   __syncthreads();
   if (t < kCombineSlice) {
     float r = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; i++) r += acc_s[i][t];
+    for (int i = 0; i < kCombineGroups; i++) r += acc_s[i][t];
     r = (L > 0.f) ? r / L : 0.f;
     if (bad) r = __builtin_nanf("");
     const int tok = c >> 3;
@@ -939,8 +944,13 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
                       dim3(D), 0, stream, c));
     return MI_OK;
   }
-  dim3 grid(nq * 8, G * (D / kCombineSlice), (unsigned)batch);
-  MI_HIP(mi::launch("attn_combine", attn_combine_kernel, grid, dim3(256), 0, stream, c));
+  if (nq > 2) {
+    MI_HIP(mi::launch("attn_combine", attn_combine_kernel<32>, dim3(nq * 8, G * (D / 32), (unsigned)batch),
+                      dim3(256), 0, stream, c));
+  } else {
+    MI_HIP(mi::launch("attn_combine", attn_combine_kernel<16>, dim3(nq * 8, G * (D / 16), (unsigned)batch),
+                      dim3(256), 0, stream, c));
+  }
   return MI_OK;
 }
 
