@@ -302,7 +302,6 @@ attn_split_kernel(SplitArgs a, X x) {
   RopeTab<X::kSH> tab;
   HeadPart<kProj ? D / kTPH : 4> qpart;
   f16x8 kf[2][8], vf[16];
-  int64_t kfirst = key_begin + 32 * w;
   if constexpr (kProj) {
     qpart.load(x.q_proj + ((int64_t)blockIdx.y * GH * 8 + threadIdx.x / kTPH) * (2 * D), x.q_w,
                lane);
@@ -374,7 +373,6 @@ attn_split_kernel(SplitArgs a, X x) {
     lim0 = len;
     key_begin = 32 * (max(t_lo, ps) - ps);
     key_end = min(32 * (min(t_hi, pe) - ps), len);
-    kfirst = key_begin + 32 * w;
     pslot = (int64_t)chunk_idx + s;
   }
 
@@ -454,7 +452,14 @@ attn_split_kernel(SplitArgs a, X x) {
       for (int e = 0; e < 8; e++)
         if (e >= valid) vf[dblk][e] = (_Float16)0.f;
   };
-  for (int64_t k0 = kfirst; k0 < key_end; k0 += 32 * NWH) {
+  // Wave w of the head takes a contiguous run of the range's 32-key tiles
+  // (ceil(tiles / NWH) each).  Against tiles dealt round-robin this took the
+  // C2 split from 14.6 to 14.2 us (one tile per wave either way: the loop
+  // the compiler makes is what differs); verify and the ragged batch are
+  // unchanged.
+  const int64_t per_wave = ((key_end - key_begin + 31) / 32 + NWH - 1) / NWH;
+  const int64_t kw_end = min(key_begin + 32 * per_wave * (w + 1), key_end);
+  for (int64_t k0 = key_begin + 32 * per_wave * w; k0 < kw_end; k0 += 32) {
     load_k(k0, kf);
     load_v(k0, vf);
     if (!flat && k0 + 32 > key_end) zero_v_tail(k0);
