@@ -231,7 +231,8 @@ mi_status mi_attn_decode_ragged(const mi_f16* k_rows, const mi_f16* v_rows,
  * nothing; a batch whose mi_attn_ragged_workspace_size exceeds the array
  * returns MI_ERR_UNSUPPORTED.  Every call on one device shares that
  * device's array: calls that overlap in time on one device (other streams
- * or threads) race on it and must be serialised by the caller.  Same
+ * or threads) race on it and must be serialised by the caller.  The stream
+ * must belong to the current device (MI_ERR_INVALID_ARG otherwise).  Same
  * arguments and results as mi_attn_decode_ragged otherwise.
  * No counterpart in the reference (whose decode is single-sequence). */
 mi_status mi_attn_decode_ragged_noalloc(const mi_f16* k_rows, const mi_f16* v_rows,
