@@ -427,6 +427,7 @@ def main():
                "us_per_layer": us2, "c1_us_per_layer": us1,
                "c1_gbps": C1_BYTES / (us1 * 1e3),
                "cpu_model": cpu_model(), "host_nproc": os.cpu_count(), "threads_used": 1,
+               "build": O.build_flags(),
                "sample": f"C2 shape: {runs2} single-thread decodes (ctx 32768, gated) in "
                          f"{el2:.1f} s; C1: {runs1} decodes (ctx 512) in {el1:.1f} s; the C "
                          f"restatement of src/math_util.rs:264-269, 323-383 on f32 inputs "
@@ -459,6 +460,12 @@ def main():
         e = traffic.get(key)
         return None if e is None else e["read_bytes"] + e["write_bytes"]
 
+    # The traffic figures are not measured in this run: they come from the
+    # committed counter runs, at the commit recorded in the file.
+    traffic_src = ("profiles/traffic.json@" + str(traffic.get("commit", "unknown"))
+                   + " (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-scaled; not this run)"
+                   if traffic else None)
+
     if d:
         line["decode_us_per_layer"] = round(d["us_per_layer"], 3)
         ach = C2_BYTES / (d["split_kernel_us"] * 1e3)
@@ -466,6 +473,7 @@ def main():
                             "achieved": round(ach, 1), "peak": hbm_peak, "unit": "GB/s",
                             "frac": round(ach / hbm_peak, 4),
                             "traffic": traffic_of("decode_split_c2"),
+                            "traffic_source": traffic_src,
                             # the whole call (append + split + combine, launch gaps
                             # included): algorithmic bytes / step time per layer
                             "whole_call_achieved": round(d["gbps"], 1),
@@ -478,7 +486,8 @@ def main():
                                     "achieved": round(p["tflops_kernel"], 1), "peak": f16_peak,
                                     "unit": "TFLOP/s",
                                     "frac": round(p["tflops_kernel"] / f16_peak, 4),
-                                    "traffic": traffic_of("prefill_c4")}
+                                    "traffic": traffic_of("prefill_c4"),
+                                    "traffic_source": traffic_src}
         line["prefill"] = {k2: (round(v2, 3) if isinstance(v2, float) else v2)
                            for k2, v2 in p.items()}
     vr = rec.get("verify")
@@ -488,6 +497,7 @@ def main():
                                    "achieved": round(ach, 1), "peak": hbm_peak, "unit": "GB/s",
                                    "frac": round(ach / hbm_peak, 4),
                                    "traffic": traffic_of("verify_split_c5"),
+                            "traffic_source": traffic_src,
                                    "whole_call_achieved": round(vr["gbps"], 1),
                                    "whole_call_frac": round(vr["gbps"] / hbm_peak, 4)}
     for key in ("verify", "ragged", "oproj"):
@@ -500,7 +510,8 @@ def main():
         line["roofline_oproj"] = {"bound": "hbm", "kernel": "matvec_bf16_kernel (o_proj 2048x4096)",
                                   "achieved": round(ach, 1), "peak": hbm_peak, "unit": "GB/s",
                                   "frac": round(ach / hbm_peak, 4),
-                                  "traffic": traffic_of("oproj_bf16")}
+                                  "traffic": traffic_of("oproj_bf16"),
+                                    "traffic_source": traffic_src}
     line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
 

@@ -20,8 +20,9 @@
  *     the handle's workspace are large enough, so they can be captured.  A
  *     call that would have to grow either while its stream is capturing
  *     returns MI_ERR_INVALID_ARG; make one eager call of the largest size
- *     (or mi_kv_reserve) first.  A workspace replaced by a larger one is
- *     kept until mi_kv_destroy, so graphs captured earlier stay valid; cache
+ *     (or mi_kv_reserve) first.  A workspace replaced by a larger one after
+ *     a capture used it is kept until mi_kv_destroy, so graphs captured
+ *     earlier stay valid (one never captured is freed when replaced); cache
  *     growth (mi_kv_reserve, or an append past capacity) moves the K/V
  *     buffers and invalidates every graph captured on the handle.
  *   - A handle belongs to the device that is current at mi_kv_create; calls
@@ -220,8 +221,10 @@ mi_status mi_attn_decode_ragged(const mi_f16* k_rows, const mi_f16* v_rows,
 
 /* Bytes of the device-resident scratch array behind
  * mi_attn_decode_ragged_noalloc (one copy per device, held until the process
- * ends): 16 MiB, which covers batches up to ~760 sequences at the Qwen3.6
- * shape (16 query / 2 KV heads, head_dim 256). */
+ * ends): 16 MiB, which covers batches up to 887 sequences at the Qwen3.6
+ * shape (16 query / 2 KV heads, head_dim 256) with the default split (one KV
+ * head per workgroup); MI_ATTN_SPLIT_GH=2 lowers that to 759.  The exact
+ * test is mi_attn_ragged_workspace_size(...) <= MI_NOALLOC_SCRATCH_BYTES. */
 #define MI_NOALLOC_SCRATCH_BYTES (16u << 20)
 
 /* mi_attn_decode_ragged without a workspace argument, for callers that

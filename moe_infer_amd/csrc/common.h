@@ -161,8 +161,10 @@ struct mi_kv {
   // Split-K decode / verify partials, grown on demand and kept for reuse.
   void* ws = nullptr;
   size_t ws_bytes = 0;
-  // Workspaces replaced by a larger one; freed at mi_kv_destroy (graphs
-  // captured before the growth still address them).
+  // A graph capture has enqueued work that uses ws.
+  bool ws_captured = false;
+  // Workspaces replaced by a larger one after a capture used them; freed at
+  // mi_kv_destroy (graphs captured before the growth still address them).
   std::vector<void*> ws_retired;
 };
 

@@ -457,9 +457,8 @@ attn_split_kernel(SplitArgs a, X x) {
   // C2 split from 14.6 to 14.2 us (one tile per wave either way: the loop
   // the compiler makes is what differs); verify and the ragged batch are
   // unchanged.
-  const int64_t per_wave = ((key_end - key_begin + 31) / 32 + NWH - 1) / NWH;
-  const int64_t kw_end = min(key_begin + 32 * per_wave * (w + 1), key_end);
-  for (int64_t k0 = key_begin + 32 * per_wave * w; k0 < kw_end; k0 += 32) {
+  const mi::WaveTiles wt = mi::split_wave_tiles(key_begin, key_end, NWH, w);
+  for (int64_t k0 = wt.first; k0 < wt.last; k0 += 32) {
     load_k(k0, kf);
     load_v(k0, vf);
     if (!flat && k0 + 32 > key_end) zero_v_tail(k0);
@@ -968,12 +967,20 @@ mi_status cache_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float
                        _Float16* out, int64_t past_pos, int32_t n, hipStream_t stream,
                        const _Float16* k_new = nullptr, const _Float16* v_new = nullptr) {
   const int64_t lim0 = past_pos + 1;
+  // The workspace is grown once, to the largest group's need, before any
+  // launch: a growth refused under graph capture then leaves nothing of
+  // this call half-recorded.
+  size_t need = 0;
+  for (int32_t t0 = 0; t0 < n; t0 += 4) {
+    const int nq = (n - t0) < 4 ? (n - t0) : 4;
+    const SplitPlan plan = plan_split(past_pos + t0 + nq, 1, kv->G, nq);
+    need = std::max(need, split_workspace_bytes(1, kv->G, plan.max_chunks, nq));
+  }
+  void* ws;
+  MI_TRY(mi::kv_workspace(kv, need, stream, &ws));
   for (int32_t t0 = 0; t0 < n; t0 += 4) {
     const int nq = (n - t0) < 4 ? (n - t0) : 4;
     const int64_t rows = past_pos + t0 + nq;  // rows the last token of this group sees
-    const SplitPlan plan = plan_split(rows, 1, kv->G, nq);
-    void* ws;
-    MI_TRY(mi::kv_workspace(kv, split_workspace_bytes(1, kv->G, plan.max_chunks, nq), stream, &ws));
     const int64_t qoff = (int64_t)t0 * kv->H * D;
     AppendRows app;
     if (k_new) {

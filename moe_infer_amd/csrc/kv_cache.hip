@@ -224,18 +224,28 @@ mi_status no_capture(hipStream_t stream, const char* what) {
   return MI_OK;
 }
 
-// A grown workspace replaces the old one, which is kept (not freed) until
-// mi_kv_destroy: graphs captured earlier hold its address and stay valid.
+// A grown workspace replaces the old one.  If a graph capture has used the
+// old one, it is kept (not freed) until mi_kv_destroy: the captured graph
+// holds its address and stays valid.  Otherwise it is freed at once
+// (hipFree waits for the device work that may still use it).
 mi_status kv_workspace(mi_kv* kv, size_t bytes, hipStream_t stream, void** ws) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  MI_HIP(hipStreamIsCapturing(stream, &cs));
+  const bool capturing = cs != hipStreamCaptureStatusNone;
   if (bytes > kv->ws_bytes) {
     MI_TRY(no_capture(stream, "the split-K workspace"));
     void* p = nullptr;
     const size_t b = bytes + bytes / 4;
     MI_HIP(hipMalloc(&p, b));
-    if (kv->ws) kv->ws_retired.push_back(kv->ws);
+    if (kv->ws) {
+      if (kv->ws_captured) kv->ws_retired.push_back(kv->ws);
+      else MI_HIP(hipFree(kv->ws));
+    }
     kv->ws = p;
     kv->ws_bytes = b;
+    kv->ws_captured = false;
   }
+  if (capturing) kv->ws_captured = true;
   *ws = kv->ws;
   return MI_OK;
 }

@@ -60,7 +60,51 @@ MI_HD inline bool prefill_steady(const PrefillWave& p, int t, bool pending) {
   return prefill_active(p, t) && pending && !prefill_diag(p, t) && t + 1 < p.nt;
 }
 
+// The 64-queries-per-wave form (attn_prefill64_kernel): wave (qb, kp) owns
+// queries q0 + 64 qb .. + 63 and keys 32 kp .. 32 kp + 31 of every 64-key
+// tile; the workgroup walks the same nt tiles as above.
+struct PrefillWave64 {
+  int first, last, kv_len, nt;
+  int koff;  // 32 kp: the wave's key half of a tile
+};
+
+MI_HD inline PrefillWave64 prefill_wave64(int past, int n, int qtile, int qb, int kp) {
+  PrefillWave64 p;
+  const int q0 = qtile * kPrefillBQ;
+  p.first = past + q0 + 64 * qb;
+  p.last = p.first + 63;
+  p.kv_len = past + n;
+  const int end = past + q0 + kPrefillBQ < p.kv_len ? past + q0 + kPrefillBQ : p.kv_len;
+  p.nt = (end + kPrefillBK - 1) / kPrefillBK;
+  p.koff = 32 * kp;
+  return p;
+}
+MI_HD inline bool prefill64_active(const PrefillWave64& p, int t) {
+  return t * kPrefillBK + p.koff <= p.last;
+}
+MI_HD inline bool prefill64_diag(const PrefillWave64& p, int t) {
+  return t * kPrefillBK + p.koff + 31 > p.first;
+}
+// As prefill_steady: the steady schedule copies K(t+1), so t + 1 < nt.
+MI_HD inline bool prefill64_steady(const PrefillWave64& p, int t, bool pending) {
+  return prefill64_active(p, t) && pending && !prefill64_diag(p, t) && t + 1 < p.nt;
+}
+
 // ----------------------------------------------------------- split-K --
+
+// The 32-key tiles wave w of nwh reads in a chunk [begin, end): a
+// contiguous run of ceil(tiles / nwh) tiles from first, while k0 < last.
+struct WaveTiles {
+  int64_t first, last;
+};
+MI_HD inline WaveTiles split_wave_tiles(int64_t begin, int64_t end, int nwh, int w) {
+  const int64_t per = ((end - begin + 31) / 32 + nwh - 1) / nwh;
+  WaveTiles r;
+  r.first = begin + 32 * per * w;
+  const int64_t e = begin + 32 * per * (w + 1);
+  r.last = e < end ? e : end;
+  return r;
+}
 
 // Most chunks (partials) per sequence of one split launch.
 constexpr int kMaxSplitChunks = 1024;

@@ -20,6 +20,9 @@
 //    block layout, so the A operand is one 128-bit LDS read, and the QK row
 //    order is chosen so that P^T is the lane's own S^T accumulator.
 //  * Epilogue: divide by the row sum, multiply by sigmoid(gate), write f16.
+#include <cstdlib>
+#include <type_traits>
+
 #include "common.h"
 #include "plan.h"
 
@@ -495,6 +498,368 @@ attn_prefill_kernel(PrefillArgs a) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// 64 queries per wave.  Workgroup = 4 waves over the same 128 queries of one
+// query head as attn_prefill_kernel, the same LDS tiles and copy schedule;
+// wave w owns query rows 64 (w & 1) .. + 63 (two 32-query MFMA column
+// blocks) and the key half kp = w >> 1 of every 64-key tile (32 keys).  Each
+// K or V fragment read from LDS then feeds two MFMAs (one per column block),
+// which halves the LDS read bytes per MFMA; O^T of 64 queries (256
+// registers) lives in the accumulation registers.  The two key halves of a
+// query row are merged through LDS at the end: wave (qb, kp) finishes column
+// block kp of its rows.
+__global__ void __launch_bounds__(256, 1)
+attn_prefill64_kernel(PrefillArgs a) {
+  extern __shared__ _Float16 lds[];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int qb = w & 1;   // query half of the workgroup's 128 rows
+  const int kp = w >> 1;  // key half of each 64-key tile
+  const int hl = lane >> 5;
+  const int col = lane & 31;
+
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7, r = bid >> 3;
+  const int jb = r >> 3;
+  const int li = (8 * jb + ((jb & 1) ? 7 - xcd : xcd)) * 8 + (r & 7);
+  if (li >= a.work) return;
+  const int hg = li & 7;
+  const int kvh = (li >> 3) % a.G;
+  const int tile_rank = (li >> 3) / a.G;
+  const int qtile = a.ntiles - 1 - tile_rank;
+  const int hq = kvh * 8 + hg;
+  const int q0 = qtile * BQ;
+
+  // Q^T operands of the two column blocks: query q0 + 64 qb + 32 b + col.
+  f16x8 qf[2][16];
+#pragma unroll
+  for (int b = 0; b < 2; b++) {
+    const int qi = q0 + 64 * qb + 32 * b + col;
+    if (qi < a.n) {
+      const _Float16* qp = a.q + ((int64_t)qi * a.H + hq) * D + 8 * hl;
+#pragma unroll
+      for (int ks = 0; ks < 16; ks++) qf[b][ks] = *(const f16x8*)(qp + 16 * ks);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 16; ks++) qf[b][ks] = f16x8{};
+    }
+  }
+  const int past = (int)a.past;
+  const mi::PrefillWave64 pw = mi::prefill_wave64(past, a.n, qtile, qb, kp);
+  const int kv_len = pw.kv_len;
+  const int nt = pw.nt;
+  const float c2 = a.scale_log2e;
+  const int qpos0 = past + q0 + 64 * qb + col;  // block b: qpos0 + 32 b
+
+  f32x16 acc[2][8];
+#pragma unroll
+  for (int b = 0; b < 2; b++)
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[b][i] = f32x16{};
+  float m[2] = {kNegBig, kNegBig}, l[2] = {0.f, 0.f};
+
+  const int lane16 = lane * 8;
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  const _Float16* kg = a.k + (int64_t)kvh * (32 * D);
+  const _Float16* vg = a.v + (int64_t)kvh * (D * 8);
+  const int64_t kblk_stride = (int64_t)a.G * (32 * D);
+  const int64_t vblk_stride = (int64_t)a.G * (D * 8);
+  _Float16* const kbuf0 = lds;
+  _Float16* const vbuf0 = lds + 2 * K_TILE_HALVES;
+  auto load_k_piece = [&](int t, int pi) {
+    const _Float16* kt = kg + (int64_t)(t * 2) * kblk_stride;
+    _Float16* ks = kbuf0 + (t & 1) * K_TILE_HALVES;
+    const int i = 8 * wu + pi;
+    const int b = i >> 4, u = (i >> 3) & 1, pc = i & 7;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        buf_rsrc(kt), (__attribute__((address_space(3))) void*)(ks + b * KSUB + u * KU + pc * 512), 16,
+        2 * (lane16 + b * (int)kblk_stride + (u * 8 + pc) * 512), 0, 0, 0);
+  };
+  auto load_v_piece = [&](int t, int pi) {
+    const _Float16* vt = vg + (int64_t)(t * 8) * vblk_stride;
+    _Float16* vs = vbuf0 + (t & 1) * V_TILE_HALVES;
+    const int i = 8 * wu + pi;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        buf_rsrc(vt), (__attribute__((address_space(3))) void*)(vs + i * 512), 16,
+        2 * (lane16 + (i >> 2) * (int)vblk_stride + (i & 3) * 512), 0, 0, 0);
+  };
+  auto zero_v_tail = [&](int t) {
+    _Float16* vs = vbuf0 + (t & 1) * V_TILE_HALVES;
+    for (int b = 0; b < 8; b++) {
+      const int valid = kv_len - (t * BK + 8 * b);
+      if (valid >= 8) continue;
+      _Float16* col8 = vs + (b * D + threadIdx.x) * 8;
+#pragma unroll
+      for (int e = 0; e < 8; e++)
+        if (e >= valid) col8[e] = (_Float16)0.f;
+    }
+  };
+  const bool tail_tile = (kv_len % BK) != 0;
+
+  const int krow = qk_row_key(col);
+  const int k_lds_off =
+      kp * KSUB + ((krow >> 2) & 1) * KU + hl * 128 + (((krow >> 3) << 2) | (krow & 3)) * 8;
+  // V fragment (step s of 16 keys, value block i of 32 columns) of this
+  // wave's key half: 8-key block 4 kp + 2 s + hl of the tile.
+  const int v_lds_off = (4 * kp + hl) * (D * 8) + col * 8;
+  auto vfrag = [&](const _Float16* vs, int idx) {  // idx = 8 s + i
+    return *(const f16x8*)(vs + 2 * (idx >> 3) * (D * 8) + (idx & 7) * 256);
+  };
+
+  f16x8 pprev[2][2];  // P^T of the previous tile: [column block][16-key step]
+  bool pending = false;
+
+  // PV of one tile outside the steady state, fragments through a ring.
+  auto pv = [&](int t) {
+    const _Float16* vs = vbuf0 + (t & 1) * V_TILE_HALVES + v_lds_off;
+    constexpr int kR = 4;
+    f16x8 vf[kR];
+#pragma unroll
+    for (int k = 0; k < kR; k++) vf[k] = vfrag(vs, k);
+#pragma unroll
+    for (int idx = 0; idx < 16; idx++) {
+      const int s = idx >> 3, i = idx & 7;
+      acc[0][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[idx % kR], pprev[0][s], acc[0][i], 0, 0, 0);
+      acc[1][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[idx % kR], pprev[1][s], acc[1][i], 0, 0, 0);
+      if (idx + kR < 16) vf[idx % kR] = vfrag(vs, idx + kR);
+    }
+  };
+  auto qk = [&](int t, f32x16 (&st)[2]) {
+    const _Float16* kr = kbuf0 + (t & 1) * K_TILE_HALVES + k_lds_off;
+    constexpr int kR = 4;
+    f16x8 ka[kR];
+    f32x16 c0 = f32x16{}, c1 = f32x16{};
+#pragma unroll
+    for (int k = 0; k < kR; k++) ka[k] = *(const f16x8*)(kr + 256 * k);
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k % kR], qf[0][k], c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k % kR], qf[1][k], c1, 0, 0, 0);
+      if (k + kR < 16) ka[k % kR] = *(const f16x8*)(kr + 256 * (k + kR));
+    }
+    st[0] = c0;
+    st[1] = c1;
+  };
+  // Weights of one column block from raw scores against reference max mm:
+  // P (f16) into p[2], returns the lane's partial row sum.
+  auto weights = [&](const f32x16& sc, float mm, f16x8 (&p)[2]) {
+    float rs = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      const f16x2 ph = {(_Float16)__builtin_amdgcn_exp2f(fmaf(sc[e], c2, -mm)),
+                        (_Float16)__builtin_amdgcn_exp2f(fmaf(sc[e + 1], c2, -mm))};
+      rs = __builtin_amdgcn_fdot2(ph, f16x2{1.f16, 1.f16}, rs, false);
+      p[e >> 3][e & 7] = ph[0];
+      p[e >> 3][(e & 7) + 1] = ph[1];
+    }
+    return rs;
+  };
+  constexpr float kLazy = 8.f;
+  auto softmax = [&](f32x16 (&st)[2], float (&alpha)[2]) {
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      float mt = st[b][0];
+#pragma unroll
+      for (int e = 1; e < 16; e++) mt = fmaxf(mt, st[b][e]);
+      mt = mi::max_xor32(mt) * c2;
+      const float mnew = (mt > m[b] + kLazy) ? mt : m[b];
+      alpha[b] = __builtin_amdgcn_exp2f(m[b] - mnew);
+      m[b] = mnew;
+      const float rs = mi::sum_xor32(weights(st[b], mnew, pprev[b]));
+      l[b] = l[b] * alpha[b] + rs;
+    }
+  };
+  // Steady-state tile: QK(t) (32 MFMAs, each K fragment feeding both column
+  // blocks, one copy piece per k-step), then PV(t-1) (32 MFMAs) with tile
+  // t's weights computed between them against the running reference max.
+  auto steady = [&](int t, float (&alpha)[2]) {
+    const _Float16* kr = kbuf0 + (t & 1) * K_TILE_HALVES + k_lds_off;
+    const _Float16* vs = vbuf0 + ((t - 1) & 1) * V_TILE_HALVES + v_lds_off;
+    constexpr int kRing = 4, vRing = 4;
+    f16x8 ka[kRing], vf[vRing];
+    f32x16 c0 = f32x16{}, c1 = f32x16{};
+#pragma unroll
+    for (int k = 0; k < kRing; k++) ka[k] = *(const f16x8*)(kr + 256 * k);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k % kRing], qf[0][k], c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k % kRing], qf[1][k], c1, 0, 0, 0);
+      if (k + kRing < 16) ka[k % kRing] = *(const f16x8*)(kr + 256 * (k + kRing));
+      if (k >= 16 - vRing) vf[k - (16 - vRing)] = vfrag(vs, k - (16 - vRing));
+      if ((k & 1) == 0) load_k_piece(t + 1, k >> 1);
+      else load_v_piece(t, k >> 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    f16x8 pnew[2][2];
+    float rs0 = 0.f, rs1 = 0.f;
+    bool ovf = false;
+#pragma unroll
+    for (int idx = 0; idx < 16; idx++) {
+      const int s = idx >> 3, i = idx & 7;
+      acc[0][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[idx % vRing], pprev[0][s], acc[0][i], 0, 0, 0);
+      acc[1][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[idx % vRing], pprev[1][s], acc[1][i], 0, 0, 0);
+      if (idx + vRing < 16) vf[idx % vRing] = vfrag(vs, idx + vRing);
+      // two weights per slot: block idx / 8, scores 2 (idx % 8), +1
+      {
+        const int b = idx >> 3, e = 2 * (idx & 7);
+        const float sa = b ? c1[e] : c0[e], sb = b ? c1[e + 1] : c0[e + 1];
+        const f16x2 ph = {(_Float16)__builtin_amdgcn_exp2f(fmaf(sa, c2, -m[b])),
+                          (_Float16)__builtin_amdgcn_exp2f(fmaf(sb, c2, -m[b]))};
+        if (b) rs1 = __builtin_amdgcn_fdot2(ph, f16x2{1.f16, 1.f16}, rs1, false);
+        else rs0 = __builtin_amdgcn_fdot2(ph, f16x2{1.f16, 1.f16}, rs0, false);
+        pnew[b][e >> 3][e & 7] = ph[0];
+        pnew[b][e >> 3][(e & 7) + 1] = ph[1];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    ovf = !(rs0 < 32768.f) || !(rs1 < 32768.f);
+    rs0 = mi::sum_xor32(rs0);
+    rs1 = mi::sum_xor32(rs1);
+    if (__ballot(ovf)) {  // rare: redo the tile's weights with the row max
+      f32x16 st[2] = {c0, c1};
+      softmax(st, alpha);
+    } else {
+      l[0] += rs0;
+      l[1] += rs1;
+#pragma unroll
+      for (int b = 0; b < 2; b++)
+#pragma unroll
+        for (int s = 0; s < 2; s++) pprev[b][s] = pnew[b][s];
+    }
+  };
+
+  // tile 0's K
+#pragma unroll
+  for (int pi = 0; pi < 8; pi++) load_k_piece(0, pi);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  for (int t = 0; t < nt; t++) {
+    const int key0 = t * BK + 32 * kp;  // first key of this wave's half
+    const bool active = mi::prefill64_active(pw, t);
+    const bool diag = mi::prefill64_diag(pw, t);
+    float alpha[2] = {1.f, 1.f};
+    if (mi::prefill64_steady(pw, t, pending)) {
+      steady(t, alpha);
+    } else {
+      if (t + 1 < nt) {
+#pragma unroll
+        for (int pi = 0; pi < 8; pi++) load_k_piece(t + 1, pi);
+      }
+#pragma unroll
+      for (int pi = 0; pi < 8; pi++) load_v_piece(t, pi);
+      f32x16 st[2];
+      if (active) qk(t, st);
+      if (pending) pv(t - 1);
+      if (active) {
+        if (diag) {  // causal mask: key (key0 + 16 (e/8) + 8 hl + e%8) <= qpos
+#pragma unroll
+          for (int b = 0; b < 2; b++) {
+            const int rel = qpos0 + 32 * b - key0 - 8 * hl;
+#pragma unroll
+            for (int e = 0; e < 16; e++)
+              if (16 * (e >> 3) + (e & 7) > rel) st[b][e] = -INFINITY;
+          }
+        }
+        softmax(st, alpha);
+      }
+    }
+    if (__ballot(alpha[0] != 1.f || alpha[1] != 1.f)) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        acc[0][i] *= alpha[0];
+        acc[1][i] *= alpha[1];
+      }
+    }
+    pending = active;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tail_tile && t + 1 == nt) {
+      zero_v_tail(t);
+      __syncthreads();
+    }
+  }
+  if (pending) pv(nt - 1);
+
+  // Merge of the two key halves: wave (qb, kp) hands column block 1 - kp to
+  // its partner through LDS and finishes block kp.  Region (qb, b) holds
+  // 32 KiB of O^T (lane-contiguous 16-byte pieces) and the (m, l) pairs.
+  // Both blocks are named at compile time (a run-time block index would
+  // turn every accumulator access into a select).
+  __syncthreads();  // every wave is done with the K/V tiles
+  float* const rgn = (float*)lds;                   // [2][2][8*4][64][4]
+  float* const mlr = rgn + 2 * 2 * 8 * 4 * 64 * 4;  // [2][2][32][2]
+  auto finish = [&](auto OB) {
+    constexpr int ob = decltype(OB)::value;  // the block this wave finishes
+    constexpr int gb = 1 - ob;               // the block it hands over
+    float* dst = rgn + (qb * 2 + gb) * (8 * 4 * 64 * 4);
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; e4++) {
+        f32x4 o = {acc[gb][i][4 * e4], acc[gb][i][4 * e4 + 1], acc[gb][i][4 * e4 + 2],
+                   acc[gb][i][4 * e4 + 3]};
+        *(f32x4*)(dst + ((i * 4 + e4) * 64 + lane) * 4) = o;
+      }
+    if (hl == 0) {
+      float* mdst = mlr + ((qb * 2 + gb) * 32 + col) * 2;
+      mdst[0] = m[gb];
+      mdst[1] = l[gb];
+    }
+    // the gate of this wave's rows in the accumulator layout: columns
+    // 32 i + 8 g + 4 hl .. + 3 of query qo
+    const int qo = q0 + 64 * qb + 32 * ob + col;
+    const bool qvalid = qo < a.n;
+    f16x4 gv[8][4];
+    if (a.gate) {
+      const _Float16* gp = a.gate + ((int64_t)(qvalid ? qo : 0) * a.H + hq) * D + 4 * hl;
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) gv[i][g4] = *(const f16x4*)(gp + 32 * i + 8 * g4);
+    }
+    mi::sync_lds();
+    const float* src = rgn + (qb * 2 + ob) * (8 * 4 * 64 * 4);
+    const float* msrc = mlr + ((qb * 2 + ob) * 32 + col) * 2;
+    const float mo = msrc[0], lo = msrc[1];
+    const float M = fmaxf(m[ob], mo);
+    const float sw = __builtin_amdgcn_exp2f(m[ob] - M), so = __builtin_amdgcn_exp2f(mo - M);
+    const float L = l[ob] * sw + lo * so;
+    const float inv = (L > 0.f) ? 1.f / L : 0.f;
+    const float fw = sw * inv, fo = so * inv;
+    _Float16* op = a.out + ((int64_t)qo * a.H + hq) * D + 4 * hl;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; g4++) {
+        const f32x4 x = *(const f32x4*)(src + ((i * 4 + g4) * 64 + lane) * 4);
+        f16x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          float v = acc[ob][i][4 * g4 + e] * fw + x[e] * fo;
+          if (a.gate) v = mi::gate_mul(v, (float)gv[i][g4][e]);
+          y[e] = (_Float16)v;
+        }
+        if (qvalid) *(f16x4*)(op + 32 * i + 8 * g4) = y;
+      }
+    }
+  };
+  if (kp == 0) finish(std::integral_constant<int, 0>{});
+  else finish(std::integral_constant<int, 1>{});
+}
+
+// Queries per wave of the prefill kernel (32: attn_prefill_kernel, 64:
+// attn_prefill64_kernel); MI_ATTN_PREFILL_QPW selects, read once per process.
+int prefill_qpw() {
+  static const int q = [] {
+    const char* e = getenv("MI_ATTN_PREFILL_QPW");
+    return (e && atoi(e) == 64) ? 64 : 32;
+  }();
+  return q;
+}
+
 }  // namespace
 
 extern "C" mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
@@ -536,9 +901,17 @@ extern "C" mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
   a.work = a.ntiles * kv->G * 8;
   a.scale_log2e = mi::kLog2e / sqrtf((float)D);
   const size_t lds = LDS_BYTES;
-  static std::atomic<uint64_t> lds_set{0};
-  MI_TRY(mi::set_lds_limit((const void*)attn_prefill_kernel, (int)lds, lds_set));
+  static_assert(LDS_BYTES >= (2 * 2 * 8 * 4 * 64 * 4 + 2 * 2 * 32 * 2) * 4,
+                "attn_prefill64_kernel's merge area fits the tile buffers");
   const int grid = (a.work + 63) / 64 * 64;
-  MI_HIP(mi::launch("attn_prefill", attn_prefill_kernel, dim3(grid), dim3(256), lds, s, a));
+  if (prefill_qpw() == 64) {
+    static std::atomic<uint64_t> lds_set64{0};
+    MI_TRY(mi::set_lds_limit((const void*)attn_prefill64_kernel, (int)lds, lds_set64));
+    MI_HIP(mi::launch("attn_prefill", attn_prefill64_kernel, dim3(grid), dim3(256), lds, s, a));
+  } else {
+    static std::atomic<uint64_t> lds_set{0};
+    MI_TRY(mi::set_lds_limit((const void*)attn_prefill_kernel, (int)lds, lds_set));
+    MI_HIP(mi::launch("attn_prefill", attn_prefill_kernel, dim3(grid), dim3(256), lds, s, a));
+  }
   return MI_OK;
 }

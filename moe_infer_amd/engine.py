@@ -58,6 +58,31 @@ def _poll(check_signal) -> None:
         raise EngineInterrupted()
 
 
+class _LayerRun:
+    """Polls check_signal before each layer and remembers the layers run.
+    On an interrupt it puts those layers' len back to the call's start
+    position before re-raising, so the rows they appended lie past len and
+    no later call (e.g. a verify with k = v = NULL, which reads len) takes
+    them for cached rows."""
+
+    def __init__(self, cache, pos, check_signal):
+        self.cache, self.pos, self.check = cache, pos, check_signal
+        self.done: list[int] = []
+
+    def __enter__(self):
+        return self
+
+    def before(self, layer) -> None:
+        _poll(self.check)
+        self.done.append(layer)
+
+    def __exit__(self, exc_type, exc, tb):
+        if exc_type is not None and issubclass(exc_type, EngineInterrupted):
+            for layer in self.done:
+                self.cache.set_len(layer, self.pos)
+        return False
+
+
 @dataclass(frozen=True)
 class EngineSnapshot:
     pos: int
@@ -119,15 +144,17 @@ class Engine:
 
         check_signal: optional callable polled before every layer; when it
         returns True the call raises EngineInterrupted and engine_pos is not
-        advanced (rows already appended by earlier layers stay past len and
-        are overwritten by the next call at the same position), as the
-        reference's per-layer poll does (fused_exp2.rs:1017-1019)."""
+        advanced, as the reference's per-layer poll does
+        (fused_exp2.rs:1017-1019); the layers already run get their len put
+        back to engine_pos, so the rows they appended lie past len and are
+        overwritten by the next call at the same position."""
         t0 = time.perf_counter()
         pos = self.cache.pos
         outs = []
-        for layer, q, k, v, gate in layers:
-            _poll(check_signal)
-            outs.append(attention.attn_step(self.cache, layer, q, k, v, pos, gate=gate))
+        with _LayerRun(self.cache, pos, check_signal) as run:
+            for layer, q, k, v, gate in layers:
+                run.before(layer)
+                outs.append(attention.attn_step(self.cache, layer, q, k, v, pos, gate=gate))
         self.cache.set_pos(pos + 1)
         self.cache.gpu_dirty = True
         self._record("engine.full_attention_ms", t0)
@@ -140,18 +167,19 @@ class Engine:
         t0 = time.perf_counter()
         pos = self.cache.pos
         outs, n = [], None
-        for layer, q, k, v, gate in layers:
-            _poll(check_signal)
-            n_l = q.numel() // (self.cache.num_q_heads * self.cache.head_dim)
-            if n is not None and n_l != n:
-                raise ValueError("every layer must carry the same token count")
-            n = n_l
-            if n == 1:
-                outs.append(attention.attn_step(self.cache, layer, q, k, v, pos, gate=gate))
-            elif n <= VERIFY_MAX_TOKENS:
-                outs.append(attention.attn_verify(self.cache, layer, q, k, v, pos, gate=gate))
-            else:
-                outs.append(attention.attn_prefill(self.cache, layer, q, k, v, pos, gate=gate))
+        with _LayerRun(self.cache, pos, check_signal) as run:
+            for layer, q, k, v, gate in layers:
+                run.before(layer)
+                n_l = q.numel() // (self.cache.num_q_heads * self.cache.head_dim)
+                if n is not None and n_l != n:
+                    raise ValueError("every layer must carry the same token count")
+                n = n_l
+                if n == 1:
+                    outs.append(attention.attn_step(self.cache, layer, q, k, v, pos, gate=gate))
+                elif n <= VERIFY_MAX_TOKENS:
+                    outs.append(attention.attn_verify(self.cache, layer, q, k, v, pos, gate=gate))
+                else:
+                    outs.append(attention.attn_prefill(self.cache, layer, q, k, v, pos, gate=gate))
         if n is not None:
             self.cache.set_pos(pos + n)
             self.cache.gpu_dirty = True
@@ -167,12 +195,13 @@ class Engine:
         t0 = time.perf_counter()
         pos = self.cache.pos
         outs = []
-        for layer, qp, k, v, qw, kw in layers:
-            _poll(check_signal)
-            outs.append(attention.attn_step_proj(self.cache, layer, qp, k, v, qw, kw, pos,
-                                                 rotary_dim=self.rotary_dim,
-                                                 rope_theta=self.rope_theta,
-                                                 eps=self.rms_norm_eps))
+        with _LayerRun(self.cache, pos, check_signal) as run:
+            for layer, qp, k, v, qw, kw in layers:
+                run.before(layer)
+                outs.append(attention.attn_step_proj(self.cache, layer, qp, k, v, qw, kw, pos,
+                                                     rotary_dim=self.rotary_dim,
+                                                     rope_theta=self.rope_theta,
+                                                     eps=self.rms_norm_eps))
         self.cache.set_pos(pos + 1)
         self.cache.gpu_dirty = True
         self._record("engine.full_attention_ms", t0)
@@ -187,24 +216,25 @@ class Engine:
         pos = self.cache.pos
         outs, n = [], None
         H, D = self.cache.num_q_heads, self.cache.head_dim
-        for layer, qp, k, v, qw, kw in layers:
-            _poll(check_signal)
-            n_l = qp.numel() // (H * 2 * D)
-            if n is not None and n_l != n:
-                raise ValueError("every layer must carry the same token count")
-            n = n_l
-            if n == 1:
-                o = attention.attn_step_proj(self.cache, layer, qp, k, v, qw, kw, pos,
-                                             rotary_dim=self.rotary_dim,
-                                             rope_theta=self.rope_theta, eps=self.rms_norm_eps)
-                outs.append(o.reshape(1, H, D))
-                continue
-            q, g = attention.qk_norm_rope_append(self.cache, layer, qp, k, v, qw, kw, pos,
+        with _LayerRun(self.cache, pos, check_signal) as run:
+            for layer, qp, k, v, qw, kw in layers:
+                run.before(layer)
+                n_l = qp.numel() // (H * 2 * D)
+                if n is not None and n_l != n:
+                    raise ValueError("every layer must carry the same token count")
+                n = n_l
+                if n == 1:
+                    o = attention.attn_step_proj(self.cache, layer, qp, k, v, qw, kw, pos,
                                                  rotary_dim=self.rotary_dim,
-                                                 rope_theta=self.rope_theta,
-                                                 eps=self.rms_norm_eps)
-            attend = attention.attn_verify if n <= VERIFY_MAX_TOKENS else attention.attn_prefill
-            outs.append(attend(self.cache, layer, q, None, None, pos, gate=g))
+                                                 rope_theta=self.rope_theta, eps=self.rms_norm_eps)
+                    outs.append(o.reshape(1, H, D))
+                    continue
+                q, g = attention.qk_norm_rope_append(self.cache, layer, qp, k, v, qw, kw, pos,
+                                                     rotary_dim=self.rotary_dim,
+                                                     rope_theta=self.rope_theta,
+                                                     eps=self.rms_norm_eps)
+                attend = attention.attn_verify if n <= VERIFY_MAX_TOKENS else attention.attn_prefill
+                outs.append(attend(self.cache, layer, q, None, None, pos, gate=g))
         if n is not None:
             self.cache.set_pos(pos + n)
             self.cache.gpu_dirty = True

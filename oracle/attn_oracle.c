@@ -24,6 +24,13 @@
 #include <stdlib.h>
 #include <string.h>
 
+#ifndef ORACLE_CFLAGS
+#define ORACLE_CFLAGS "unknown"
+#endif
+/* The compiler and flags this library was built with (reported beside the
+   CPU baseline timings). */
+const char* oracle_build_info(void) { return "gcc " __VERSION__ ", " ORACLE_CFLAGS; }
+
 #define ORACLE_API __attribute__((visibility("default")))
 
 /* ------------------------------------------------------------------ f16 -- */

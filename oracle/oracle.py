@@ -35,6 +35,7 @@ def lib() -> C.CDLL:
         L = C.CDLL(str(LIB_PATH))
         P, I64 = C.c_void_p, C.c_int64
         sigs = {
+            "oracle_build_info": (C.c_char_p, []),
             "oracle_f16_to_f32": (C.c_float, [C.c_uint16]),
             "oracle_f32_to_f16": (C.c_uint16, [C.c_float]),
             "oracle_widen_f16": (None, [P, P, I64]),
@@ -65,6 +66,11 @@ def lib() -> C.CDLL:
             fn.argtypes = args
         _lib = L
     return _lib
+
+
+def build_flags() -> str:
+    """Compiler and flags of the built oracle library."""
+    return lib().oracle_build_info().decode()
 
 
 def _p(a):

@@ -13,9 +13,10 @@
 // condition was added.
 //
 // Split-K decode / verify (attn_split_kernel, non-ragged): chunk c covers
-// keys [c * chunk, min((c+1) * chunk, len)); with P = ceil(tiles / NWH),
-// wave w of NWH reads the whole 32-key tiles k0 = begin + 32 (P w + i),
-// i = 0 .. P-1, while k0 < end.  Each tile must be 32-aligned and lie inside
+// keys [c * chunk, min((c+1) * chunk, len)); wave w of NWH reads the whole
+// 32-key tiles of mi::split_wave_tiles (the kernel calls the same helper):
+// k0 = begin + 32 (P w + i), i = 0 .. P-1, P = ceil(tiles / NWH), while
+// k0 < end.  Each tile must be 32-aligned and lie inside
 // round_cap(len) rows, every key of the chunk must be read by exactly one
 // wave, and chunks must number at most kMaxSplitChunks (the combine kernel
 // merges at most that many).
@@ -68,11 +69,10 @@ static long long split_violations(long long len, int nq, const mi::SplitKnobs& k
     const long long b = c * p.chunk;
     if (b >= len) continue;
     const long long e = b + p.chunk < len ? b + p.chunk : len;
-    const long long per = ((e - b + 31) / 32 + p.nwh - 1) / p.nwh;
     long long covered = 0;
     for (int w = 0; w < p.nwh; w++) {
-      const long long we = b + 32 * per * (w + 1) < e ? b + 32 * per * (w + 1) : e;
-      for (long long k0 = b + 32 * per * w; k0 < we; k0 += 32) {
+      const mi::WaveTiles wt = mi::split_wave_tiles(b, e, p.nwh, w);
+      for (long long k0 = wt.first; k0 < wt.last; k0 += 32) {
         if (k0 % 32 || k0 + 32 > cap) bad++;
         covered += (k0 + 32 < e ? k0 + 32 : e) - k0;
       }

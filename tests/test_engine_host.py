@@ -14,9 +14,13 @@ class FakeCache:
     def __init__(self, pos):
         self.pos = pos
         self.gpu_dirty = False
+        self.lens = {}
 
     def set_pos(self, p):
         self.pos = p
+
+    def set_len(self, layer, n):
+        self.lens[layer] = n
 
 
 class FakeTensor:
@@ -73,6 +77,8 @@ def test_interrupt_before_a_layer_raises_and_keeps_pos(method, calls):
     assert eng.engine_pos() == 41, "an interrupted call does not advance the position"
     assert state["n"] == 3, "polled once per layer, before the layer"
     assert [c[1] for c in calls if c[0] != "rope"] == [3, 7]
+    # the layers that ran (and appended rows) have their len put back to pos
+    assert eng.cache.lens == {3: 41, 7: 41}
 
 
 @pytest.mark.parametrize("method", ["forward", "forward_batched"])
