@@ -482,7 +482,7 @@ def main():
                           for k2, v2 in d.items()}
     if p:
         line["prefill_tflops"] = round(p["tflops_kernel"], 1)
-        line["roofline_prefill"] = {"bound": "mfma", "kernel": "attn_prefill_kernel (C4)",
+        line["roofline_prefill"] = {"bound": "mfma", "kernel": "attn_prefill64_kernel (C4)",
                                     "achieved": round(p["tflops_kernel"], 1), "peak": f16_peak,
                                     "unit": "TFLOP/s",
                                     "frac": round(p["tflops_kernel"] / f16_peak, 4),

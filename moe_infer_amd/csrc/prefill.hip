@@ -47,6 +47,9 @@ constexpr int LDS_HALVES = 2 * (K_TILE_HALVES + V_TILE_HALVES);
 constexpr int O_ROW = D + 4;
 constexpr int LDS_BYTES = LDS_HALVES * 2 > 4 * 32 * O_ROW * 4 ? LDS_HALVES * 2 : 4 * 32 * O_ROW * 4;
 constexpr float kNegBig = -1e30f;
+// attn_prefill64_kernel's restart flag (one int), past the tile buffers.
+constexpr int LDS_FLAG_OFF = (LDS_BYTES + 1024) / 2;  // in halves
+constexpr int LDS64_BYTES = LDS_BYTES + 1024 + 16;
 
 struct PrefillArgs {
   const _Float16* q;      // [n][H][D]
@@ -501,18 +504,23 @@ attn_prefill_kernel(PrefillArgs a) {
 
 // ---------------------------------------------------------------------------
 // 64 queries per wave.  Workgroup = 4 waves over the same 128 queries of one
-// query head as attn_prefill_kernel, the same LDS tiles and copy schedule;
-// wave w owns query rows 64 (w & 1) .. + 63 (two 32-query MFMA column
-// blocks) and the key half kp = w >> 1 of every 64-key tile (32 keys).  Each
-// K or V fragment read from LDS then feeds two MFMAs (one per column block),
-// which halves the LDS read bytes per MFMA; O^T of 64 queries (256
-// registers) lives in the accumulation registers.  The two key halves of a
-// query row are merged through LDS at the end: wave (qb, kp) finishes column
-// block kp of its rows.
+// query head as attn_prefill_kernel, with the same LDS tiles and copy
+// schedule; wave w owns query rows 64 (w & 1) .. + 63 (two 32-query MFMA
+// column blocks) and the key half kp = w >> 1 of every 64-key tile (32
+// keys).  Each K or V fragment read from LDS feeds two MFMAs (one per column
+// block), which halves the LDS read bytes per MFMA.  O^T of 64 queries is
+// 256 accumulation registers, so the scores must come out in ordinary
+// registers: the QK chain of a tile is one asm block (32 MFMAs with the K
+// fragment reads and the tile's 16 copy pieces), the rest is compiled code.
+// The two key halves of a query row merge through LDS at the end: wave
+// (qb, kp) finishes column block kp of its rows.
+
 __global__ void __launch_bounds__(256, 1)
 attn_prefill64_kernel(PrefillArgs a) {
   extern __shared__ _Float16 lds[];
   const int lane = threadIdx.x & 63;
+  // (threadIdx.x >> 6 is wave-uniform, but a readfirstlane here, making the
+  // per-tile branches scalar, leads the register allocator to ~1300 spills)
   const int w = threadIdx.x >> 6;
   const int qb = w & 1;   // query half of the workgroup's 128 rows
   const int kp = w >> 1;  // key half of each 64-key tile
@@ -559,6 +567,9 @@ attn_prefill64_kernel(PrefillArgs a) {
     for (int i = 0; i < 8; i++) acc[b][i] = f32x16{};
   float m[2] = {kNegBig, kNegBig}, l[2] = {0.f, 0.f};
 
+  // Copies: the same pieces as attn_prefill_kernel (wave w moves K pieces
+  // 8w .. 8w+7: block w / 2, row half w % 2, column chunks 0..7; and V
+  // pieces 8w .. 8w+7: 8-key blocks 2w, 2w + 1, four 1-KiB pieces each).
   const int lane16 = lane * 8;
   const int wu = __builtin_amdgcn_readfirstlane(w);
   const _Float16* kg = a.k + (int64_t)kvh * (32 * D);
@@ -567,21 +578,35 @@ attn_prefill64_kernel(PrefillArgs a) {
   const int64_t vblk_stride = (int64_t)a.G * (D * 8);
   _Float16* const kbuf0 = lds;
   _Float16* const vbuf0 = lds + 2 * K_TILE_HALVES;
+  const int kb_w = wu >> 1, ku_w = wu & 1;
+  // byte offsets of this lane within a source tile (piece 0 of the wave)
+  const int vk_off = 2 * (lane16 + kb_w * (int)kblk_stride + ku_w * 8 * 512);
+  const int vv_off = 2 * (lane16 + 2 * wu * (int)vblk_stride);
+  const int sv_off = 2 * (int)vblk_stride;
+  auto lds_addr = [](const _Float16* p) {
+    return (int)(uintptr_t)(const __attribute__((address_space(3))) _Float16*)p;
+  };
+  auto k_tile_src = [&](int t) { return buf_rsrc(kg + (int64_t)(t * 2) * kblk_stride); };
+  auto v_tile_src = [&](int t) { return buf_rsrc(vg + (int64_t)(t * 8) * vblk_stride); };
+  auto k_piece_lds = [&](int t) {  // wave's K piece 0 of tile t
+    return lds_addr(kbuf0 + (t & 1) * K_TILE_HALVES + kb_w * KSUB + ku_w * KU);
+  };
+  auto v_piece_lds = [&](int t) {
+    return lds_addr(vbuf0 + (t & 1) * V_TILE_HALVES + 8 * wu * 512);
+  };
   auto load_k_piece = [&](int t, int pi) {
-    const _Float16* kt = kg + (int64_t)(t * 2) * kblk_stride;
     _Float16* ks = kbuf0 + (t & 1) * K_TILE_HALVES;
     const int i = 8 * wu + pi;
     const int b = i >> 4, u = (i >> 3) & 1, pc = i & 7;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        buf_rsrc(kt), (__attribute__((address_space(3))) void*)(ks + b * KSUB + u * KU + pc * 512), 16,
+        k_tile_src(t), (__attribute__((address_space(3))) void*)(ks + b * KSUB + u * KU + pc * 512), 16,
         2 * (lane16 + b * (int)kblk_stride + (u * 8 + pc) * 512), 0, 0, 0);
   };
   auto load_v_piece = [&](int t, int pi) {
-    const _Float16* vt = vg + (int64_t)(t * 8) * vblk_stride;
     _Float16* vs = vbuf0 + (t & 1) * V_TILE_HALVES;
     const int i = 8 * wu + pi;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        buf_rsrc(vt), (__attribute__((address_space(3))) void*)(vs + i * 512), 16,
+        v_tile_src(t), (__attribute__((address_space(3))) void*)(vs + i * 512), 16,
         2 * (lane16 + (i >> 2) * (int)vblk_stride + (i & 3) * 512), 0, 0, 0);
   };
   auto zero_v_tail = [&](int t) {
@@ -607,10 +632,207 @@ attn_prefill64_kernel(PrefillArgs a) {
     return *(const f16x8*)(vs + 2 * (idx >> 3) * (D * 8) + (idx & 7) * 256);
   };
 
+  // S^T = K . Q^T of this wave's 32-key half of tile t for both column
+  // blocks, with the copies of K(tk) (into tile t + 1's buffer) and V(t): one asm block of 32 MFMAs
+  // (the scores must come out in ordinary registers, the compiler would
+  // give every MFMA of the kernel the accumulation-register form), the K
+  // fragments read four k-steps ahead through a ring of four, and one copy
+  // piece issued per k-step (K pieces on even steps, V on odd).  ka: LDS
+  // byte address of the lane's K fragment 0; mk / mv: LDS byte addresses of
+  // the wave's first K / V piece; vk / vv: the lane's byte offsets in the
+  // source tiles; sv: offset of the wave's second group of four V pieces.
+  // Ends with 16 wait states, since VALU code reads the results next.
+  // (m0 in the clobber list: the compiler sets m0 right before each of its
+  // own LDS copies, so nothing it holds there lives across the block.)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  auto qk = [&](int t, int tk, f32x16& c0, f32x16& c1) {
+    const int ka = lds_addr(kbuf0 + (t & 1) * K_TILE_HALVES + k_lds_off);
+    const int mk = __builtin_amdgcn_readfirstlane(k_piece_lds(t + 1));
+    const int mv = __builtin_amdgcn_readfirstlane(v_piece_lds(t));
+    const __amdgpu_buffer_rsrc_t rk = k_tile_src(tk), rv = v_tile_src(t);
+    f16x8 r0, r1, r2, r3;
+    int so;
+    asm volatile(
+    "ds_read_b128 %[r0], %[ka] offset:0\n"
+    "ds_read_b128 %[r1], %[ka] offset:512\n"
+    "ds_read_b128 %[r2], %[ka] offset:1024\n"
+    "ds_read_b128 %[r3], %[ka] offset:1536\n"
+    "s_waitcnt lgkmcnt(3)\n"
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r0], %[q0_0], 0\n"
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r0], %[q1_0], 0\n"
+    "ds_read_b128 %[r0], %[ka] offset:2048\n"
+    "s_add_u32 m0, %[mk], 0\n"
+    "s_mov_b32 %[so], 0\n"
+    "s_nop 0\n"
+    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n"
+    "s_waitcnt lgkmcnt(3)\n"
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r1], %[q0_1], %[c0]\n"
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r1], %[q1_1], %[c1]\n"
+    "ds_read_b128 %[r1], %[ka] offset:2560\n"
+    "s_add_u32 m0, %[mv], 0\n"
+    "s_mov_b32 %[so], 0\n"
+    "s_nop 0\n"
+    "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
+    "s_waitcnt lgkmcnt(3)\n"
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r2], %[q0_2], %[c0]\n"
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r2], %[q1_2], %[c1]\n"
+    "ds_read_b128 %[r2], %[ka] offset:3072\n"
+    "s_add_u32 m0, %[mk], 1024\n"
+    "s_movk_i32 %[so], 1024\n"
+    "s_nop 0\n"
+    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n"
+    "s_waitcnt lgkmcnt(3)\n"
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r3], %[q0_3], %[c0]\n"
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r3], %[q1_3], %[c1]\n"
+    "ds_read_b128 %[r3], %[ka] offset:3584\n"
+    "s_add_u32 m0, %[mv], 1024\n"
+    "s_movk_i32 %[so], 1024\n"
+    "s_nop 0\n"
+    "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
+    "s_waitcnt lgkmcnt(3)\n"
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r0], %[q0_4], %[c0]\n"
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r0], %[q1_4], %[c1]\n"
+    "ds_read_b128 %[r0], %[ka] offset:4096\n"
+    "s_add_u32 m0, %[mk], 2048\n"
+    "s_movk_i32 %[so], 2048\n"
+    "s_nop 0\n"
+    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n"
+    "s_waitcnt lgkmcnt(3)\n"
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r1], %[q0_5], %[c0]\n"
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r1], %[q1_5], %[c1]\n"
+    "ds_read_b128 %[r1], %[ka] offset:4608\n"
+    "s_add_u32 m0, %[mv], 2048\n"
+    "s_movk_i32 %[so], 2048\n"
+    "s_nop 0\n"
+    "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
+    "s_waitcnt lgkmcnt(3)\n"
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r2], %[q0_6], %[c0]\n"
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r2], %[q1_6], %[c1]\n"
+    "ds_read_b128 %[r2], %[ka] offset:5120\n"
+    "s_add_u32 m0, %[mk], 3072\n"
+    "s_movk_i32 %[so], 3072\n"
+    "s_nop 0\n"
+    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n"
+    "s_waitcnt lgkmcnt(3)\n"
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r3], %[q0_7], %[c0]\n"
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r3], %[q1_7], %[c1]\n"
+    "ds_read_b128 %[r3], %[ka] offset:5632\n"
+    "s_add_u32 m0, %[mv], 3072\n"
+    "s_movk_i32 %[so], 3072\n"
+    "s_nop 0\n"
+    "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
+    "s_waitcnt lgkmcnt(3)\n"
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r0], %[q0_8], %[c0]\n"
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r0], %[q1_8], %[c1]\n"
+    "ds_read_b128 %[r0], %[ka] offset:6144\n"
+    "s_add_u32 m0, %[mk], 4096\n"
+    "s_movk_i32 %[so], 4096\n"
+    "s_nop 0\n"
+    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n"
+    "s_waitcnt lgkmcnt(3)\n"
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r1], %[q0_9], %[c0]\n"
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r1], %[q1_9], %[c1]\n"
+    "ds_read_b128 %[r1], %[ka] offset:6656\n"
+    "s_add_u32 m0, %[mv], 4096\n"
+    "s_add_u32 %[so], %[sv], 0\n"
+    "s_nop 0\n"
+    "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
+    "s_waitcnt lgkmcnt(3)\n"
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r2], %[q0_10], %[c0]\n"
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r2], %[q1_10], %[c1]\n"
+    "ds_read_b128 %[r2], %[ka] offset:7168\n"
+    "s_add_u32 m0, %[mk], 5120\n"
+    "s_movk_i32 %[so], 5120\n"
+    "s_nop 0\n"
+    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n"
+    "s_waitcnt lgkmcnt(3)\n"
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r3], %[q0_11], %[c0]\n"
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r3], %[q1_11], %[c1]\n"
+    "ds_read_b128 %[r3], %[ka] offset:7680\n"
+    "s_add_u32 m0, %[mv], 5120\n"
+    "s_add_u32 %[so], %[sv], 1024\n"
+    "s_nop 0\n"
+    "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
+    "s_waitcnt lgkmcnt(3)\n"
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r0], %[q0_12], %[c0]\n"
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r0], %[q1_12], %[c1]\n"
+    "s_add_u32 m0, %[mk], 6144\n"
+    "s_movk_i32 %[so], 6144\n"
+    "s_nop 0\n"
+    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n"
+    "s_waitcnt lgkmcnt(2)\n"
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r1], %[q0_13], %[c0]\n"
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r1], %[q1_13], %[c1]\n"
+    "s_add_u32 m0, %[mv], 6144\n"
+    "s_add_u32 %[so], %[sv], 2048\n"
+    "s_nop 0\n"
+    "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
+    "s_waitcnt lgkmcnt(1)\n"
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r2], %[q0_14], %[c0]\n"
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r2], %[q1_14], %[c1]\n"
+    "s_add_u32 m0, %[mk], 7168\n"
+    "s_movk_i32 %[so], 7168\n"
+    "s_nop 0\n"
+    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n"
+    "s_waitcnt lgkmcnt(0)\n"
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r3], %[q0_15], %[c0]\n"
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r3], %[q1_15], %[c1]\n"
+    "s_add_u32 m0, %[mv], 7168\n"
+    "s_add_u32 %[so], %[sv], 3072\n"
+    "s_nop 0\n"
+    "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
+    "s_nop 15\n"
+        : [c0] "=&v"(c0), [c1] "=&v"(c1), [r0] "=&v"(r0), [r1] "=&v"(r1), [r2] "=&v"(r2),
+          [r3] "=&v"(r3), [so] "=&s"(so)
+        : [ka] "v"(ka), [mk] "s"(mk), [mv] "s"(mv), [rk] "s"(rk), [rv] "s"(rv),
+          [vk] "v"(vk_off), [vv] "v"(vv_off), [sv] "s"(sv_off),
+          [q0_0] "v"(qf[0][0]), [q0_1] "v"(qf[0][1]), [q0_2] "v"(qf[0][2]), [q0_3] "v"(qf[0][3]),
+          [q0_4] "v"(qf[0][4]), [q0_5] "v"(qf[0][5]), [q0_6] "v"(qf[0][6]), [q0_7] "v"(qf[0][7]),
+          [q0_8] "v"(qf[0][8]), [q0_9] "v"(qf[0][9]), [q0_10] "v"(qf[0][10]), [q0_11] "v"(qf[0][11]),
+          [q0_12] "v"(qf[0][12]), [q0_13] "v"(qf[0][13]), [q0_14] "v"(qf[0][14]), [q0_15] "v"(qf[0][15]),
+          [q1_0] "v"(qf[1][0]), [q1_1] "v"(qf[1][1]), [q1_2] "v"(qf[1][2]), [q1_3] "v"(qf[1][3]),
+          [q1_4] "v"(qf[1][4]), [q1_5] "v"(qf[1][5]), [q1_6] "v"(qf[1][6]), [q1_7] "v"(qf[1][7]),
+          [q1_8] "v"(qf[1][8]), [q1_9] "v"(qf[1][9]), [q1_10] "v"(qf[1][10]), [q1_11] "v"(qf[1][11]),
+          [q1_12] "v"(qf[1][12]), [q1_13] "v"(qf[1][13]), [q1_14] "v"(qf[1][14]), [q1_15] "v"(qf[1][15])
+        : "m0", "memory");
+  };
+#pragma clang diagnostic pop
+  auto tile_max = [&](const f32x16& sc) {
+    float mt = sc[0];
+#pragma unroll
+    for (int e = 1; e < 16; e++) mt = fmaxf(mt, sc[e]);
+    return mi::max_xor32(mt) * c2;
+  };
+  // Weights of one column block against reference max mm into p (f16);
+  // returns the lane's partial row sum.
+  auto weights = [&](const f32x16& sc, float mm, f16x8 (&p)[2]) {
+    float rs = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      const f16x2 ph = {(_Float16)__builtin_amdgcn_exp2f(fmaf(sc[e], c2, -mm)),
+                        (_Float16)__builtin_amdgcn_exp2f(fmaf(sc[e + 1], c2, -mm))};
+      rs = __builtin_amdgcn_fdot2(ph, f16x2{1.f16, 1.f16}, rs, false);
+      p[e >> 3][e & 7] = ph[0];
+      p[e >> 3][(e & 7) + 1] = ph[1];
+    }
+    return rs;
+  };
+  // Causal mask of a diagonal half tile: key (key0 + 16 (e/8) + 8 hl + e%8)
+  // is visible to query qpos0 + 32 b.
+  auto mask = [&](int t, f32x16& c0, f32x16& c1) {
+    const int key0 = t * BK + 32 * kp;
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      const int rel = qpos0 + 32 * b - key0 - 8 * hl;
+      f32x16& sc = b ? c1 : c0;
+#pragma unroll
+      for (int e = 0; e < 16; e++)
+        if (16 * (e >> 3) + (e & 7) > rel) sc[e] = -INFINITY;
+    }
+  };
+  // PV of tile t alone (the wave has no keys in the next tile).
   f16x8 pprev[2][2];  // P^T of the previous tile: [column block][16-key step]
-  bool pending = false;
-
-  // PV of one tile outside the steady state, fragments through a ring.
   auto pv = [&](int t) {
     const _Float16* vs = vbuf0 + (t & 1) * V_TILE_HALVES + v_lds_off;
     constexpr int kR = 4;
@@ -625,161 +847,167 @@ attn_prefill64_kernel(PrefillArgs a) {
       if (idx + kR < 16) vf[idx % kR] = vfrag(vs, idx + kR);
     }
   };
-  auto qk = [&](int t, f32x16 (&st)[2]) {
-    const _Float16* kr = kbuf0 + (t & 1) * K_TILE_HALVES + k_lds_off;
-    constexpr int kR = 4;
-    f16x8 ka[kR];
-    f32x16 c0 = f32x16{}, c1 = f32x16{};
+
+  // The reference max m of a column is fixed for the whole walk: the max
+  // of the wave's first tile, so weights 2^(s - m) are never rescaled and O
+  // needs no rescaling either (every VALU touch of the 256 accumulation
+  // registers would move them out of those registers).  Weights stay in f16
+  // range while no score exceeds m by 15 or more (base 2); if one does, the
+  // workgroup starts over: a max pass (QK only) takes the exact row max
+  // over every visible key, and the walk is redone against it, where no
+  // weight exceeds 1.  Only valid query columns count (padding columns past
+  // n may see stale rows).  Benign data never pays for the restart.
+  const bool valid0 = q0 + 64 * qb + col < a.n, valid1 = q0 + 64 * qb + 32 + col < a.n;
+  int* const ovf_word = (int*)(lds + LDS_FLAG_OFF);  // set by a wave whose weights overflowed
+  bool pending = false;
+  if (threadIdx.x == 0) ovf_word[0] = 0;  // published by tile 0's barrier
+  // The walk over the tiles; against the exact max (after a restart) it
+  // neither checks for nor reports overflow.  Returns whether the workgroup
+  // must start over.
+  auto walk = [&](bool exact) {
 #pragma unroll
-    for (int k = 0; k < kR; k++) ka[k] = *(const f16x8*)(kr + 256 * k);
+    for (int b = 0; b < 2; b++)
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-      c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k % kR], qf[0][k], c0, 0, 0, 0);
-      c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k % kR], qf[1][k], c1, 0, 0, 0);
-      if (k + kR < 16) ka[k % kR] = *(const f16x8*)(kr + 256 * (k + kR));
-    }
-    st[0] = c0;
-    st[1] = c1;
-  };
-  // Weights of one column block from raw scores against reference max mm:
-  // P (f16) into p[2], returns the lane's partial row sum.
-  auto weights = [&](const f32x16& sc, float mm, f16x8 (&p)[2]) {
-    float rs = 0.f;
+      for (int i = 0; i < 8; i++) acc[b][i] = f32x16{};
+    // Tile 0: K(0) first, then QK(0) with the copies of K(1) (K(0) again
+    // when it is the only tile) and V(0).
 #pragma unroll
-    for (int e = 0; e < 16; e += 2) {
-      const f16x2 ph = {(_Float16)__builtin_amdgcn_exp2f(fmaf(sc[e], c2, -mm)),
-                        (_Float16)__builtin_amdgcn_exp2f(fmaf(sc[e + 1], c2, -mm))};
-      rs = __builtin_amdgcn_fdot2(ph, f16x2{1.f16, 1.f16}, rs, false);
-      p[e >> 3][e & 7] = ph[0];
-      p[e >> 3][(e & 7) + 1] = ph[1];
-    }
-    return rs;
-  };
-  constexpr float kLazy = 8.f;
-  auto softmax = [&](f32x16 (&st)[2], float (&alpha)[2]) {
-#pragma unroll
-    for (int b = 0; b < 2; b++) {
-      float mt = st[b][0];
-#pragma unroll
-      for (int e = 1; e < 16; e++) mt = fmaxf(mt, st[b][e]);
-      mt = mi::max_xor32(mt) * c2;
-      const float mnew = (mt > m[b] + kLazy) ? mt : m[b];
-      alpha[b] = __builtin_amdgcn_exp2f(m[b] - mnew);
-      m[b] = mnew;
-      const float rs = mi::sum_xor32(weights(st[b], mnew, pprev[b]));
-      l[b] = l[b] * alpha[b] + rs;
-    }
-  };
-  // Steady-state tile: QK(t) (32 MFMAs, each K fragment feeding both column
-  // blocks, one copy piece per k-step), then PV(t-1) (32 MFMAs) with tile
-  // t's weights computed between them against the running reference max.
-  auto steady = [&](int t, float (&alpha)[2]) {
-    const _Float16* kr = kbuf0 + (t & 1) * K_TILE_HALVES + k_lds_off;
-    const _Float16* vs = vbuf0 + ((t - 1) & 1) * V_TILE_HALVES + v_lds_off;
-    constexpr int kRing = 4, vRing = 4;
-    f16x8 ka[kRing], vf[vRing];
-    f32x16 c0 = f32x16{}, c1 = f32x16{};
-#pragma unroll
-    for (int k = 0; k < kRing; k++) ka[k] = *(const f16x8*)(kr + 256 * k);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-      c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k % kRing], qf[0][k], c0, 0, 0, 0);
-      c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k % kRing], qf[1][k], c1, 0, 0, 0);
-      if (k + kRing < 16) ka[k % kRing] = *(const f16x8*)(kr + 256 * (k + kRing));
-      if (k >= 16 - vRing) vf[k - (16 - vRing)] = vfrag(vs, k - (16 - vRing));
-      if ((k & 1) == 0) load_k_piece(t + 1, k >> 1);
-      else load_v_piece(t, k >> 1);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    f16x8 pnew[2][2];
-    float rs0 = 0.f, rs1 = 0.f;
-    bool ovf = false;
-#pragma unroll
-    for (int idx = 0; idx < 16; idx++) {
-      const int s = idx >> 3, i = idx & 7;
-      acc[0][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[idx % vRing], pprev[0][s], acc[0][i], 0, 0, 0);
-      acc[1][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[idx % vRing], pprev[1][s], acc[1][i], 0, 0, 0);
-      if (idx + vRing < 16) vf[idx % vRing] = vfrag(vs, idx + vRing);
-      // two weights per slot: block idx / 8, scores 2 (idx % 8), +1
-      {
-        const int b = idx >> 3, e = 2 * (idx & 7);
-        const float sa = b ? c1[e] : c0[e], sb = b ? c1[e + 1] : c0[e + 1];
-        const f16x2 ph = {(_Float16)__builtin_amdgcn_exp2f(fmaf(sa, c2, -m[b])),
-                          (_Float16)__builtin_amdgcn_exp2f(fmaf(sb, c2, -m[b]))};
-        if (b) rs1 = __builtin_amdgcn_fdot2(ph, f16x2{1.f16, 1.f16}, rs1, false);
-        else rs0 = __builtin_amdgcn_fdot2(ph, f16x2{1.f16, 1.f16}, rs0, false);
-        pnew[b][e >> 3][e & 7] = ph[0];
-        pnew[b][e >> 3][(e & 7) + 1] = ph[1];
+    for (int pi = 0; pi < 8; pi++) load_k_piece(0, pi);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    {
+      f32x16 c0, c1;
+      qk(0, nt > 1 ? 1 : 0, c0, c1);
+      if (mi::prefill64_diag(pw, 0)) mask(0, c0, c1);
+      if (!exact) {  // a column with no visible key keeps kNegBig (weights 0)
+        m[0] = fmaxf(tile_max(c0), kNegBig);
+        m[1] = fmaxf(tile_max(c1), kNegBig);
       }
-      __builtin_amdgcn_sched_barrier(0);
+      l[0] = mi::sum_xor32(weights(c0, m[0], pprev[0]));
+      l[1] = mi::sum_xor32(weights(c1, m[1], pprev[1]));
+      pending = true;
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (tail_tile && nt == 1) {
+        zero_v_tail(0);
+        __syncthreads();
+      }
     }
-    ovf = !(rs0 < 32768.f) || !(rs1 < 32768.f);
-    rs0 = mi::sum_xor32(rs0);
-    rs1 = mi::sum_xor32(rs1);
-    if (__ballot(ovf)) {  // rare: redo the tile's weights with the row max
-      f32x16 st[2] = {c0, c1};
-      softmax(st, alpha);
-    } else {
-      l[0] += rs0;
-      l[1] += rs1;
+    for (int t = 1; t < nt; t++) {
+      const int tk = t + 1 < nt ? t + 1 : t;  // K copy source (t + 1, or a repeat)
+      bool ovf = false;
+      if (mi::prefill64_active(pw, t)) {  // implies pending
+        const _Float16* vs = vbuf0 + ((t - 1) & 1) * V_TILE_HALVES + v_lds_off;
+        constexpr int vRing = 4;
+        f32x16 c0, c1;
+        qk(t, tk, c0, c1);
+        if (mi::prefill64_diag(pw, t)) mask(t, c0, c1);  // wave-uniform
+        // PV(t-1), with tile t's weights computed between its MFMAs.
+        f16x8 vf[vRing];
 #pragma unroll
-      for (int b = 0; b < 2; b++)
+        for (int k = 0; k < vRing; k++) vf[k] = vfrag(vs, k);
+        f16x8 pnew[2][2];
+        float rs0 = 0.f, rs1 = 0.f;
+        // Slot idx: two MFMAs, with the slot's two weights (scores 2 idx,
+        // 2 idx + 1 of the 32) spread around them and pipelined one slot
+        // deep, so that no VALU op waits for the one just before it (a wave
+        // issues in order; after each MFMA about two FMAs and one
+        // exponential issue in its shadow):
+        //   after MFMA 0: exp(a_idx), fma(a_idx+1), cvt(idx-1)
+        //   after MFMA 1: exp(b_idx), fma(b_idx+1), dot2(idx-1)
+        auto score = [&](int j) {  // raw score j of the 32 (block j / 16)
+          const int bb = j >> 4, ee = j & 15;
+          return bb ? c1[ee] : c0[ee];
+        };
+        float ya = fmaf(score(0), c2, -m[0]), yb = fmaf(score(1), c2, -m[0]);
+        float xa_prev = 0.f, xb_prev = 0.f;
+        f16x2 ph_prev = {};
 #pragma unroll
-        for (int s = 0; s < 2; s++) pprev[b][s] = pnew[b][s];
+        for (int idx = 0; idx < 17; idx++) {
+          const int s = idx >> 3, i = idx & 7;
+          if (idx < 16)
+            acc[0][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[idx % vRing], pprev[0][s], acc[0][i], 0, 0, 0);
+          float xa = 0.f, ya_next = 0.f;
+          if (idx < 16) xa = __builtin_amdgcn_exp2f(ya);
+          if (idx < 15) ya_next = fmaf(score(2 * idx + 2), c2, -m[(idx + 1) >> 3]);
+          if (idx > 0) ph_prev = f16x2{(_Float16)xa_prev, (_Float16)xb_prev};
+          __builtin_amdgcn_sched_barrier(0);
+          if (idx < 16) {
+            acc[1][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[idx % vRing], pprev[1][s], acc[1][i], 0, 0, 0);
+            if (idx + vRing < 16) vf[idx % vRing] = vfrag(vs, idx + vRing);
+          }
+          float xb = 0.f, yb_next = 0.f;
+          if (idx < 16) xb = __builtin_amdgcn_exp2f(yb);
+          if (idx < 15) yb_next = fmaf(score(2 * idx + 3), c2, -m[(idx + 1) >> 3]);
+          if (idx > 0) {
+            const int jp = idx - 1, bp = jp >> 3, ep = 2 * (jp & 7);
+            if (bp) rs1 = __builtin_amdgcn_fdot2(ph_prev, f16x2{1.f16, 1.f16}, rs1, false);
+            else rs0 = __builtin_amdgcn_fdot2(ph_prev, f16x2{1.f16, 1.f16}, rs0, false);
+            pnew[bp][ep >> 3][ep & 7] = ph_prev[0];
+            pnew[bp][ep >> 3][(ep & 7) + 1] = ph_prev[1];
+          }
+          xa_prev = xa;
+          xb_prev = xb;
+          ya = ya_next;
+          yb = yb_next;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        // a weight of 2^15 or more (each is at most its lane's sum) leaves
+        // f16 range; also inf / NaN
+        ovf = (valid0 && !(rs0 < 32768.f)) || (valid1 && !(rs1 < 32768.f));
+        l[0] += mi::sum_xor32(rs0);
+        l[1] += mi::sum_xor32(rs1);
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+          for (int s = 0; s < 2; s++) pprev[b][s] = pnew[b][s];
+        pending = true;
+      } else {
+        if (t + 1 < nt) {
+#pragma unroll
+          for (int pi = 0; pi < 8; pi++) load_k_piece(t + 1, pi);
+        }
+#pragma unroll
+        for (int pi = 0; pi < 8; pi++) load_v_piece(t, pi);
+        if (pending) pv(t - 1);
+        pending = false;
+      }
+      if (!exact && __ballot(ovf)) ovf_word[0] = 1;
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (tail_tile && t + 1 == nt) {
+        zero_v_tail(t);
+        __syncthreads();
+      }
     }
+    // read after the last barrier: the same for every wave
+    return !exact && ovf_word[0] != 0;
   };
-
-  // tile 0's K
+  if (walk(false)) {
+    // Max pass: every tile's QK, masked, folded into m (the V copies of the
+    // asm block land and are not read).
+    __syncthreads();  // every wave has read the flag word
+    m[0] = m[1] = kNegBig;
 #pragma unroll
-  for (int pi = 0; pi < 8; pi++) load_k_piece(0, pi);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  for (int t = 0; t < nt; t++) {
-    const int key0 = t * BK + 32 * kp;  // first key of this wave's half
-    const bool active = mi::prefill64_active(pw, t);
-    const bool diag = mi::prefill64_diag(pw, t);
-    float alpha[2] = {1.f, 1.f};
-    if (mi::prefill64_steady(pw, t, pending)) {
-      steady(t, alpha);
-    } else {
-      if (t + 1 < nt) {
+    for (int pi = 0; pi < 8; pi++) load_k_piece(0, pi);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int t = 0; t < nt; t++) {
+      const int tk = t + 1 < nt ? t + 1 : t;
+      if (mi::prefill64_active(pw, t)) {
+        f32x16 c0, c1;
+        qk(t, tk, c0, c1);
+        if (mi::prefill64_diag(pw, t)) mask(t, c0, c1);
+        m[0] = fmaxf(m[0], tile_max(c0));
+        m[1] = fmaxf(m[1], tile_max(c1));
+      } else if (t + 1 < nt) {
 #pragma unroll
         for (int pi = 0; pi < 8; pi++) load_k_piece(t + 1, pi);
       }
-#pragma unroll
-      for (int pi = 0; pi < 8; pi++) load_v_piece(t, pi);
-      f32x16 st[2];
-      if (active) qk(t, st);
-      if (pending) pv(t - 1);
-      if (active) {
-        if (diag) {  // causal mask: key (key0 + 16 (e/8) + 8 hl + e%8) <= qpos
-#pragma unroll
-          for (int b = 0; b < 2; b++) {
-            const int rel = qpos0 + 32 * b - key0 - 8 * hl;
-#pragma unroll
-            for (int e = 0; e < 16; e++)
-              if (16 * (e >> 3) + (e & 7) > rel) st[b][e] = -INFINITY;
-          }
-        }
-        softmax(st, alpha);
-      }
-    }
-    if (__ballot(alpha[0] != 1.f || alpha[1] != 1.f)) {
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        acc[0][i] *= alpha[0];
-        acc[1][i] *= alpha[1];
-      }
-    }
-    pending = active;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tail_tile && t + 1 == nt) {
-      zero_v_tail(t);
+      __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
     }
+    walk(true);
   }
   if (pending) pv(nt - 1);
 
@@ -808,18 +1036,8 @@ attn_prefill64_kernel(PrefillArgs a) {
       mdst[0] = m[gb];
       mdst[1] = l[gb];
     }
-    // the gate of this wave's rows in the accumulator layout: columns
-    // 32 i + 8 g + 4 hl .. + 3 of query qo
     const int qo = q0 + 64 * qb + 32 * ob + col;
     const bool qvalid = qo < a.n;
-    f16x4 gv[8][4];
-    if (a.gate) {
-      const _Float16* gp = a.gate + ((int64_t)(qvalid ? qo : 0) * a.H + hq) * D + 4 * hl;
-#pragma unroll
-      for (int i = 0; i < 8; i++)
-#pragma unroll
-        for (int g4 = 0; g4 < 4; g4++) gv[i][g4] = *(const f16x4*)(gp + 32 * i + 8 * g4);
-    }
     mi::sync_lds();
     const float* src = rgn + (qb * 2 + ob) * (8 * 4 * 64 * 4);
     const float* msrc = mlr + ((qb * 2 + ob) * 32 + col) * 2;
@@ -829,35 +1047,70 @@ attn_prefill64_kernel(PrefillArgs a) {
     const float L = l[ob] * sw + lo * so;
     const float inv = (L > 0.f) ? 1.f / L : 0.f;
     const float fw = sw * inv, fo = so * inv;
-    _Float16* op = a.out + ((int64_t)qo * a.H + hq) * D + 4 * hl;
+    // Output: lane (col, hl) holds columns 32 i + 8 g + 4 hl .. + 3 of
+    // query qo; a v_permlane32_swap between the two lane halves gives lane
+    // hl all eight columns of chunk (i, g = 2 j + hl), so every lane writes
+    // whole 16-byte chunks (half the store instructions of 8-byte pieces).
+    _Float16* op = a.out + ((int64_t)qo * a.H + hq) * D;
+    const _Float16* gp = a.gate ? a.gate + ((int64_t)(qvalid ? qo : 0) * a.H + hq) * D : nullptr;
+    auto swap32 = [](float& lo, float& hi) {  // lo of the upper half <-> hi of the lower half
+      auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+      lo = __uint_as_float(r[0]);
+      hi = __uint_as_float(r[1]);
+    };
+    auto store = [&](auto GATED) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
+      for (int i = 0; i < 8; i++) {
 #pragma unroll
-      for (int g4 = 0; g4 < 4; g4++) {
-        const f32x4 x = *(const f32x4*)(src + ((i * 4 + g4) * 64 + lane) * 4);
-        f16x4 y;
+        for (int j = 0; j < 2; j++) {
+          // y[k][e]: value e of chunk (i, 2 j + k) held by this lane
+          float y[2][4];
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          float v = acc[ob][i][4 * g4 + e] * fw + x[e] * fo;
-          if (a.gate) v = mi::gate_mul(v, (float)gv[i][g4][e]);
-          y[e] = (_Float16)v;
+          for (int k = 0; k < 2; k++) {
+            const int g4 = 2 * j + k;
+            const f32x4 x = *(const f32x4*)(src + ((i * 4 + g4) * 64 + lane) * 4);
+#pragma unroll
+            for (int e = 0; e < 4; e++) y[k][e] = acc[ob][i][4 * g4 + e] * fw + x[e] * fo;
+          }
+          // lane half 0 keeps chunk 2j (its columns 0..3, receives 4..7);
+          // lane half 1 keeps chunk 2j + 1 (receives 0..3, its 4..7)
+#pragma unroll
+          for (int e = 0; e < 4; e++) swap32(y[0][e], y[1][e]);
+          // now lane half 0: y[0] = columns 0..3, y[1] = 4..7 of chunk 2j;
+          // lane half 1: y[0] = columns 0..3, y[1] = 4..7 of chunk 2j + 1
+          const int cofs = 32 * i + 8 * (2 * j + hl);
+          f16x8 h;
+          if constexpr (decltype(GATED)::value) {
+            const f16x8 g = *(const f16x8*)(gp + cofs);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              h[e] = (_Float16)mi::gate_mul(y[0][e], (float)g[e]);
+              h[4 + e] = (_Float16)mi::gate_mul(y[1][e], (float)g[4 + e]);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              h[e] = (_Float16)y[0][e];
+              h[4 + e] = (_Float16)y[1][e];
+            }
+          }
+          if (qvalid) *(f16x8*)(op + cofs) = h;
         }
-        if (qvalid) *(f16x4*)(op + 32 * i + 8 * g4) = y;
       }
-    }
+    };
+    if (a.gate) store(std::true_type{});
+    else store(std::false_type{});
   };
   if (kp == 0) finish(std::integral_constant<int, 0>{});
   else finish(std::integral_constant<int, 1>{});
 }
 
-// Queries per wave of the prefill kernel (32: attn_prefill_kernel, 64:
-// attn_prefill64_kernel); MI_ATTN_PREFILL_QPW selects, read once per process.
+// Queries per wave of the prefill kernel: 64 (attn_prefill64_kernel, the
+// default) or 32 (attn_prefill_kernel, MI_ATTN_PREFILL_QPW=32: the earlier
+// form, kept for comparison).  Read at each call.
 int prefill_qpw() {
-  static const int q = [] {
-    const char* e = getenv("MI_ATTN_PREFILL_QPW");
-    return (e && atoi(e) == 64) ? 64 : 32;
-  }();
-  return q;
+  const char* e = getenv("MI_ATTN_PREFILL_QPW");
+  return (e && atoi(e) == 32) ? 32 : 64;
 }
 
 }  // namespace
@@ -901,13 +1154,14 @@ extern "C" mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
   a.work = a.ntiles * kv->G * 8;
   a.scale_log2e = mi::kLog2e / sqrtf((float)D);
   const size_t lds = LDS_BYTES;
-  static_assert(LDS_BYTES >= (2 * 2 * 8 * 4 * 64 * 4 + 2 * 2 * 32 * 2) * 4,
-                "attn_prefill64_kernel's merge area fits the tile buffers");
+  static_assert(LDS_FLAG_OFF * 2 >= (2 * 2 * 8 * 4 * 64 * 4 + 2 * 2 * 32 * 2) * 4,
+                "attn_prefill64_kernel's merge area lies below its restart flag");
   const int grid = (a.work + 63) / 64 * 64;
   if (prefill_qpw() == 64) {
     static std::atomic<uint64_t> lds_set64{0};
-    MI_TRY(mi::set_lds_limit((const void*)attn_prefill64_kernel, (int)lds, lds_set64));
-    MI_HIP(mi::launch("attn_prefill", attn_prefill64_kernel, dim3(grid), dim3(256), lds, s, a));
+    MI_TRY(mi::set_lds_limit((const void*)attn_prefill64_kernel, LDS64_BYTES, lds_set64));
+    MI_HIP(mi::launch("attn_prefill", attn_prefill64_kernel, dim3(grid), dim3(256),
+                      (size_t)LDS64_BYTES, s, a));
   } else {
     static std::atomic<uint64_t> lds_set{0};
     MI_TRY(mi::set_lds_limit((const void*)attn_prefill_kernel, (int)lds, lds_set));

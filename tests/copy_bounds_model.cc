@@ -59,6 +59,39 @@ static long long prefill_violations(int past, int n, long long cap, bool old_rul
   return bad;
 }
 
+// The same for attn_prefill64_kernel: every pass (the walk, and after an
+// overflow the max pass and the walk again) copies K(0) first; tile 0's asm
+// block copies K(min(1, nt - 1)) and V(0); at tile t >= 1 an active wave
+// (mi::prefill64_active) copies K(min(t + 1, nt - 1)) and V(t) in its asm
+// block, any other copies K(t + 1) when t + 1 < nt, and V(t) (the max pass:
+// K only).  Both passes are walked.
+static long long prefill64_violations(int past, int n, long long cap) {
+  long long bad = 0;
+  auto copy = [&](int T) {
+    if ((long long)T * mi::kPrefillBK + mi::kPrefillBK > cap) bad++;
+  };
+  const int ntiles = (n + mi::kPrefillBQ - 1) / mi::kPrefillBQ;
+  for (int qt = 0; qt < ntiles; qt++)
+    for (int w = 0; w < 4; w++) {
+      const mi::PrefillWave64 p = mi::prefill_wave64(past, n, qt, w & 1, w >> 1);
+      const int nt = p.nt;
+      for (int pass = 0; pass < 2; pass++) {  // 0: walk, 1: max pass
+        copy(0);
+        for (int t = 0; t < nt; t++) {
+          const int tk = t + 1 < nt ? t + 1 : t;
+          if (t == 0 || mi::prefill64_active(p, t)) {
+            copy(tk);
+            copy(t);  // V(t), also in the max pass's asm block
+          } else {
+            if (t + 1 < nt) copy(t + 1);
+            if (pass == 0) copy(t);
+          }
+        }
+      }
+    }
+  return bad;
+}
+
 // Tiles of one split launch over `len` rows with `nq` query tokens.
 static long long split_violations(long long len, int nq, const mi::SplitKnobs& k) {
   const mi::SplitPlan p = mi::plan_split(len, 1, 2, nq, k);
@@ -84,21 +117,24 @@ static long long split_violations(long long len, int nq, const mi::SplitKnobs& k
 }
 
 int main() {
-  long long cases = 0, bad_new = 0, bad_old = 0;
+  long long cases = 0, bad_new = 0, bad_old = 0, bad64 = 0;
   for (int past = 0; past < 700; past++)
     for (int n = 1; n < 700; n++) {
       const long long cap = round_cap((long long)past + n);
       bad_new += prefill_violations(past, n, cap, false);
       bad_old += prefill_violations(past, n, cap, true);
+      bad64 += prefill64_violations(past, n, cap);
       cases++;
     }
   std::printf("prefill %lld %lld\n", cases, bad_new);
   std::printf("prefill_without_last_tile_rule %lld %lld\n", cases, bad_old);
+  std::printf("prefill64 %lld %lld\n", cases, bad64);
   // long pasts and C4-adjacent sizes
   long long c2 = 0, b2 = 0;
   for (int past : {0, 32768, 65000, 65535, 131071})
     for (int n : {1, 127, 128, 129, 257, 1000, 4095, 4096, 4097}) {
       b2 += prefill_violations(past, n, round_cap((long long)past + n), false);
+      b2 += prefill64_violations(past, n, round_cap((long long)past + n));
       c2++;
     }
   std::printf("prefill_long %lld %lld\n", c2, b2);

@@ -1,7 +1,8 @@
 """The kernels' reads stay inside the cache allocation, checked on the CPU
 by a model of their tile walks compiled against the launch-plan header the
 kernels themselves use (moe_infer_amd/csrc/plan.h): the causal prefill's
-global -> LDS tile copies over (past, n) in [0, 700)^2 and at long pasts,
+global -> LDS tile copies (both kernel forms, the 64-query one over both of
+its passes) over (past, n) in [0, 700)^2 and at long pasts,
 and the split-K decode / verify tile loads over lengths 1..5000 and long
 contexts under several planning knobs.  The prefill walk without the
 steady schedule's last-tile rule must find out-of-allocation copies (the
@@ -34,6 +35,11 @@ def model_output(tmp_path_factory):
 
 def test_prefill_tile_copies_stay_inside_the_allocation(model_output):
     cases, bad = model_output["prefill"]
+    assert cases == 700 * 699 and bad == 0
+
+
+def test_prefill64_tile_copies_stay_inside_the_allocation(model_output):
+    cases, bad = model_output["prefill64"]
     assert cases == 700 * 699 and bad == 0
 
 

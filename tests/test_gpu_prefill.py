@@ -135,3 +135,50 @@ def test_prefill_long_past_and_c4_adjacent(past, n):
         attn_decode(c, 0, qd[i], past + i + 1, gate=gd[i], out=dec[i])
     assert_close(out, host(dec), f"prefill past={past} n={n}: all rows vs GPU decode",
                  atol=1e-3)
+
+
+@pytest.mark.parametrize("n,past", [(1, 0), (129, 0), (200, 77), (300, 1000), (1000, 31)])
+def test_prefill_32_query_kernel_matches(n, past, monkeypatch):
+    """The earlier 32-queries-per-wave kernel (MI_ATTN_PREFILL_QPW=32, read
+    at each call) against the oracle, and against the default 64-query
+    kernel on the same inputs."""
+    announce(f"prefill qpw=32 n={n} past={past}")
+    rng = np.random.default_rng(3 * n + past)
+    kp, vp = f16(rng, past, G * D), f16(rng, past, G * D)
+    q, k, v, g = f16(rng, n, H, D), f16(rng, n, G * D), f16(rng, n, G * D), f16(rng, n, H, D)
+    outs = []
+    for qpw in ("32", "64"):
+        monkeypatch.setenv("MI_ATTN_PREFILL_QPW", qpw)
+        c = Cache(num_layers=1, capacity=past + n)
+        if past:
+            c.upload(0, kp, vp)
+            c.set_pos(past)
+        outs.append(host(attn_prefill(c, 0, dev(q), dev(k), dev(v), past, gate=dev(g))))
+    ref = O.causal(q, np.concatenate([kp, k]), np.concatenate([vp, v]), past, gate=g)
+    assert_close(outs[0], ref, f"prefill qpw=32 n={n} past={past}")
+    assert_close(outs[0], outs[1], f"prefill qpw=32 vs 64 n={n} past={past}", atol=1e-3)
+
+
+def test_prefill_restart_after_late_large_scores():
+    """Key 300 scores ~20 (base 2) above the first tile's keys for every
+    query of KV group 0 (each query has a component along r, the key is 28 r):
+    with the 64-query kernel's reference max fixed at the first tile, that
+    weight would leave f16 range, so the workgroups start over against the
+    exact row max.  Output on the oracle (rows past 300 are dominated by
+    v[300]), every row finite."""
+    announce("prefill late large scores n=700")
+    n = 700
+    rng = np.random.default_rng(12)
+    r = rng.standard_normal(D)
+    r /= np.linalg.norm(r)
+    q = rng.standard_normal((n, H, D)).astype(np.float32)
+    q[:, :8, :] += 8.0 * r
+    q = q.astype(np.float16)
+    k = f16(rng, n, G * D)
+    k[300, :D] = (28.0 * r).astype(np.float16)
+    v = f16(rng, n, G * D)
+    c = Cache(num_layers=1, capacity=n)
+    out = host(attn_prefill(c, 0, dev(q), dev(k), dev(v), 0))
+    assert np.all(np.isfinite(out))
+    for i in [0, 299, 300, 301, 383, 384, 450, 511, 512, 640, 699]:
+        assert_close(out[i], O.decode(q[i].ravel(), k, v, i + 1), f"late large scores row {i}")
