@@ -163,6 +163,12 @@ struct mi_kv {
   size_t ws_bytes = 0;
   // A graph capture has enqueued work that uses ws.
   bool ws_captured = false;
+  // State of the split kernel's in-launch merge (counters, per-XCD
+  // partials; zeroed at creation, reset by the kernels themselves), and
+  // whether this device dispatches workgroup b to XCD b % 8 (probed at
+  // creation; the merge is used only then).
+  void* mstate = nullptr;
+  bool merge_ok = false;
   // Workspaces replaced by a larger one after a capture used them; freed at
   // mi_kv_destroy (graphs captured before the growth still address them).
   std::vector<void*> ws_retired;
@@ -180,6 +186,11 @@ mi_status kv_workspace(mi_kv* kv, size_t bytes, hipStream_t stream, void** ws);
 // Grows the cache to at least `rows` rows (mi_kv_reserve), refused while
 // `stream` is capturing a graph.
 mi_status kv_grow(mi_kv* kv, int64_t rows, hipStream_t stream);
+// Bytes of mi_kv::mstate for G KV heads (decode.hip).
+size_t merge_state_bytes(int G);
+// Whether workgroup b of a launch runs on XCD b % 8 on the current device,
+// checked once per device with a probe kernel (decode.hip).
+bool xcd_round_robin();
 // Enqueues the row copy of kv_cache_append_n on `stream` (no len update).
 mi_status kv_append_rows(mi_kv* kv, int32_t layer, const _Float16* k,
                          const _Float16* v, int64_t pos, int32_t n,

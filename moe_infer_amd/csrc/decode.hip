@@ -68,6 +68,16 @@ struct SplitArgs {
   _Float16* vw;
   int64_t app0;
   int app_n;
+  // In-launch merge (single sequence, one query token, one KV head per
+  // workgroup): partials m / l at part_ml with a 256-byte stride per slot,
+  // then merged inside the launch (merge_tail) and written to out with the
+  // gate, instead of by attn_combine_kernel.  Null mcnt: off.
+  int* mcnt;          // counters: XCD-local [G][8], then per KV head [G] (256 B apart)
+  float* xo;          // per-XCD partials [G][8][8][D]
+  float* xml;         // per-XCD (m, l) [G][8][64]
+  const _Float16* gate;
+  const float* gate32;
+  _Float16* out;
 };
 
 // Partials are consumed once, by the combine kernel: streaming stores
@@ -201,6 +211,172 @@ struct HeadPart {
   }
 };
 
+// ---- in-launch merge of the chunk partials (decode of one sequence, one
+// query token, one KV head per workgroup).  Workgroup b of the launch runs on
+// XCD b % 8 (round-robin dispatch; checked per device when a handle is
+// created, else the merge is not used).  The partials of the chunks of one
+// KV head whose workgroups share an XCD are merged by the last of them to
+// arrive (an XCD-local counter: stores and atomics meet in that XCD's L2,
+// so no cache write-back is needed); it writes one partial per XCD through
+// to memory, and the last of those (a device-scope counter) merges the
+// eight, normalises, applies the gate and writes the output.  Every counter
+// is reset by its last user, so the launch can be replayed in a graph.
+// Off by default (decode_merge_enabled): in a probe of the protocol alone it
+// added 1.9 us to a launch of 256 workgroups, but after a real C2 split the
+// chain takes ~5 us, as long as the combine launch.
+
+// Loads without waiting (the caller waits, see wait_regs).  Within the XCD
+// a plain load: it misses this CU's L1 (which never held those lines in this
+// launch; L1 and L2 are invalidated at every kernel start) and hits the
+// XCD's L2, where the members' stores landed.  Across XCDs sc0 sc1 (the
+// data was written through to memory).
+__device__ __forceinline__ f32x4 ld_xcd4(const float* p) {
+  f32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ __forceinline__ float ld_xcd1(const float* p) {
+  float v;
+  asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ __forceinline__ f32x4 ld_dev4(const float* p) {
+  f32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off sc0 sc1" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ __forceinline__ float ld_dev1(const float* p) {
+  float v;
+  asm volatile("global_load_dword %0, %1, off sc0 sc1" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ __forceinline__ void st_dev4(float* p, f32x4 v) {  // written through to memory
+  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st_dev1(float* p, float v) {
+  asm volatile("global_store_dword %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
+}
+// Waits for this thread's outstanding loads; the empty asm statements make
+// every later use of the loaded registers follow the wait.
+template <int N>
+__device__ __forceinline__ void wait_regs(f32x4 (&o)[N], float (&m)[N], float (&l)[N]) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; i++) asm volatile("" : "+v"(o[i]), "+v"(m[i]), "+v"(l[i]));
+}
+
+constexpr int kMergeStride = 64;  // ints between counters (256 bytes)
+
+template <int NT>
+__device__ void merge_tail(const SplitArgs& a) {
+  static_assert(NT == 512, "one f32x4 of the 8 x 256 outputs per thread");
+  const int t = threadIdx.x;
+  const int hy = blockIdx.y;  // KV head
+  const int mc = a.max_chunks;
+  const int x = (blockIdx.x + mc * hy) & 7;  // this workgroup's XCD
+  const int ngroups = mc < 8 ? mc : 8;
+  // chunks c of this head on XCD x: c = first(x) + 8 j
+  auto first_of = [&](int xx) { return ((xx - mc * hy) % 8 + 8) % 8; };
+  const int first = first_of(x);
+  const int nmem = first < mc ? (mc - first + 7) / 8 : 0;
+  const int col = t >> 6, d4 = (t & 63) * 4;  // output column (query head) and values
+  __shared__ int s_last;
+
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have reached L2
+  __syncthreads();
+  if (t == 0)
+    s_last = __hip_atomic_fetch_add(a.mcnt + (hy * 8 + x) * kMergeStride, 1, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_WORKGROUP) == nmem - 1;
+  __syncthreads();
+  if (!s_last) return;
+
+  // XCD level: online merge of the members' (m, l, o), 16 at a time
+  float M = kNegBig, L = 0.f;
+  f32x4 O = {0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < nmem; j0 += 16) {
+    f32x4 o[16];
+    float m[16], l[16];
+#pragma unroll
+    for (int u = 0; u < 16; u++) {
+      const int c = first + 8 * (j0 + u < nmem ? j0 + u : j0);
+      const int64_t slot = (int64_t)hy * a.nslots + c;
+      o[u] = ld_xcd4(a.part_o + (slot * 8 + col) * D + d4);
+      m[u] = ld_xcd1(a.part_ml + slot * 64 + 2 * col);
+      l[u] = ld_xcd1(a.part_ml + slot * 64 + 2 * col + 1);
+    }
+    wait_regs(o, m, l);
+    float mb = M;
+#pragma unroll
+    for (int u = 0; u < 16; u++)
+      if (j0 + u < nmem) mb = fmaxf(mb, m[u]);
+    const float r = exp2f(M - mb);
+    L *= r;
+    O *= r;
+#pragma unroll
+    for (int u = 0; u < 16; u++)
+      if (j0 + u < nmem) {
+        const float w = exp2f(m[u] - mb);
+        L += l[u] * w;
+        O += o[u] * w;
+      }
+    M = mb;
+  }
+  st_dev4(a.xo + ((hy * 8 + x) * 8 + col) * D + d4, O);
+  if (d4 == 0) {
+    st_dev1(a.xml + (hy * 8 + x) * 64 + 2 * col, M);
+    st_dev1(a.xml + (hy * 8 + x) * 64 + 2 * col + 1, L);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // written through before the arrival is counted
+  __syncthreads();
+  if (t == 0) {
+    __hip_atomic_store(a.mcnt + (hy * 8 + x) * kMergeStride, 0, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_WORKGROUP);
+    int* dc = a.mcnt + (a.G * 8 + hy) * kMergeStride;
+    const bool last = __hip_atomic_fetch_add(dc, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      ngroups - 1;
+    if (last) __hip_atomic_store(dc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+
+  // head level: the XCDs that hold chunks of this head
+  f32x4 o[8];
+  float m[8], l[8];
+#pragma unroll
+  for (int xx = 0; xx < 8; xx++) {
+    o[xx] = ld_dev4(a.xo + ((hy * 8 + xx) * 8 + col) * D + d4);
+    m[xx] = ld_dev1(a.xml + (hy * 8 + xx) * 64 + 2 * col);
+    l[xx] = ld_dev1(a.xml + (hy * 8 + xx) * 64 + 2 * col + 1);
+  }
+  wait_regs(o, m, l);
+  float Mh = kNegBig;
+#pragma unroll
+  for (int xx = 0; xx < 8; xx++)
+    if (first_of(xx) < mc) Mh = fmaxf(Mh, m[xx]);
+  float Lh = 0.f;
+  f32x4 Oh = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int xx = 0; xx < 8; xx++)
+    if (first_of(xx) < mc) {
+      const float w = exp2f(m[xx] - Mh);
+      Lh += l[xx] * w;
+      Oh += o[xx] * w;
+    }
+  // out = O / L (zero when L = 0, math_util.rs:357, 372), then the gate
+  const float inv = Lh > 0.f ? 1.f / Lh : 0.f;
+  const int hq = hy * 8 + col;
+  f16x4 h;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    float r = Oh[e] * inv;
+    if (a.gate) r = mi::gate_mul(r, (float)a.gate[hq * D + d4 + e]);
+    else if (a.gate32) r = mi::gate_mul(r, a.gate32[hq * (2 * D) + D + d4 + e]);
+    h[e] = (_Float16)r;
+  }
+  *(f16x4*)(a.out + hq * D + d4) = h;
+}
+
 // Workgroup = GH KV heads x NWH waves per head, over one chunk of keys of one
 // sequence (with GH = 2 a workgroup reads one contiguous stretch of both
 // heads' K and V blocks).  NCB column blocks of 16 columns (column c = token
@@ -257,7 +433,9 @@ attn_split_kernel(SplitArgs a, X x) {
   }
   if constexpr (!flat) {
     key_begin = (int64_t)chunk_idx * a.chunk;
-    if (key_begin >= len) return;  // uniform over the workgroup
+    // uniform over the workgroup; with the in-launch merge every workgroup
+    // takes part (an empty chunk leaves an empty partial)
+    if (key_begin >= len && !a.mcnt) return;
     key_end = min(key_begin + (int64_t)a.chunk, len);
   }
 
@@ -557,13 +735,28 @@ attn_split_kernel(SplitArgs a, X x) {
       o += *(const f32x4*)(so2 + (ww * ncols + c) * kLdsRow + d4) * sc;
     }
     const int64_t pb = ((int64_t)(blockIdx.y * GH + h2) * a.nslots + pslot) * ncols + c;
-    if (d4 == 0) {
-      store_part(M, a.part_ml + pb * 2 + 0);
-      store_part(L, a.part_ml + pb * 2 + 1);
+    if (!flat && a.mcnt) {
+      // plain stores: the merging workgroup reads them from this XCD's L2
+      if (d4 == 0) {
+        float* ml = a.part_ml + ((int64_t)(blockIdx.y * GH + h2) * a.nslots + pslot) * 64 + 2 * c;
+        ml[0] = M;
+        ml[1] = L;
+      }
+      *(f32x4*)(a.part_o + pb * D + d4) = o;
+    } else {
+      if (d4 == 0) {
+        store_part(M, a.part_ml + pb * 2 + 0);
+        store_part(L, a.part_ml + pb * 2 + 1);
+      }
+      store_part(o, (f32x4*)(a.part_o + pb * D + d4));
     }
-    store_part(o, (f32x4*)(a.part_o + pb * D + d4));
   }
-  if constexpr (!flat) break;
+  if constexpr (!flat) {
+    if constexpr (NWH * GH == 8 && NCB == 1) {  // the forms the host merges in-launch
+      if (a.mcnt) merge_tail<NWH * GH * 64>(a);
+    }
+    break;
+  }
   if (__builtin_amdgcn_readfirstlane(a.tile_off[s + 1]) >= t_hi) break;
   // next sequence with tiles (the range ends inside a later one)
   do s++;
@@ -818,7 +1011,8 @@ mi_status launch_split(const SplitArgs& a, int64_t batch, hipStream_t stream, co
   size_t lds = (size_t)GH * (NWH * ncols * (D + 4) + 2 * NWH * ncols) * sizeof(float);
   if constexpr (is_proj<X>::value) lds += (size_t)GH * 8 * (D + 8) * sizeof(_Float16);
   static std::atomic<uint64_t> lds_set{0};
-  MI_TRY(mi::set_lds_limit((const void*)attn_split_kernel<NWH, NCB, GH, X, FLAT>, 160 * 1024, lds_set));
+  // (below 160 KiB: the kernel also holds a few bytes of static LDS)
+  MI_TRY(mi::set_lds_limit((const void*)attn_split_kernel<NWH, NCB, GH, X, FLAT>, 159 * 1024, lds_set));
   dim3 grid(a.max_chunks, a.G / GH, (unsigned)batch);
   MI_HIP(mi::launch("attn_split", attn_split_kernel<NWH, NCB, GH, X, FLAT>, grid,
                     dim3(NWH * GH * 64), lds, stream, a, x));
@@ -837,6 +1031,30 @@ mi_status launch_proj(const SplitArgs& a, const SplitPlan& plan, hipStream_t str
 size_t split_workspace_bytes(int64_t batch, int G, int max_chunks, int nq) {
   size_t units = (size_t)batch * G * max_chunks * nq * 8;
   return units * (D + 2) * sizeof(float) + 256;
+}
+
+// The in-launch merge: partials o as usual, then (m, l) with a 256-byte
+// stride per slot (workgroups of neighbouring slots run on different XCDs,
+// whose L2s must not share a line); the state in mi_kv::mstate: counters,
+// then per-XCD partials [G][8][8][D] and (m, l) [G][8][64].
+size_t merge_workspace_bytes(int G, int max_chunks) {
+  return (size_t)G * max_chunks * (8 * D + 64) * sizeof(float) + 256;
+}
+size_t merge_counter_bytes(int G) { return ((size_t)9 * G * kMergeStride * sizeof(int) + 4095) / 4096 * 4096; }
+// The workspace a cache decode / verify launch asks for.
+size_t attend_workspace_bytes(int G, int max_chunks, int nq) {
+  const size_t s = split_workspace_bytes(1, G, max_chunks, nq);
+  return nq == 1 ? std::max(s, merge_workspace_bytes(G, max_chunks)) : s;
+}
+// MI_ATTN_DECODE_MERGE=1 (read at each call) merges single-token decode
+// inside the split launch; off by default: at C2 the merge chain after the
+// last workgroup (store acknowledgement, XCD-local arrival, merge from L2,
+// write-through, device arrival, final merge from memory) takes ~5 us, as
+// long as the second launch it replaces (measured: 21.9 against 19.9 us per
+// step on one box, 18.5-18.7 against ~18 us for the kernel end).
+bool decode_merge_enabled() {
+  const char* e = getenv("MI_ATTN_DECODE_MERGE");
+  return e && *e && atoi(e) == 1;
 }
 
 // Flat ragged split: workgroups per KV-head group (one per CU), and the
@@ -859,9 +1077,11 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
                     int64_t max_len, int64_t batch, int H, int G, int nq,
                     const _Float16* q, const _Float16* gate, _Float16* out,
                     void* ws, size_t ws_bytes, hipStream_t stream,
-                    const AppendRows& app = AppendRows(), const ProjArgs* proj = nullptr) {
+                    const AppendRows& app = AppendRows(), const ProjArgs* proj = nullptr,
+                    const mi_kv* kv = nullptr) {
   const SplitPlan plan = plan_split(max_len, batch, G, nq);
   SplitArgs a;
+  a.mcnt = nullptr;
   a.k = k;
   a.v = v;
   a.offsets = offsets;
@@ -904,6 +1124,20 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
     a.max_chunks = nwg;
     a.chunk = 0;
   }
+  // In-launch merge: one sequence, one query token, one KV head per
+  // workgroup, 8 waves (the launch_split<8, 1, 1> forms), on a device that
+  // dispatches round-robin over 8 XCDs, with room for the padded (m, l).
+  const bool merge = kv && kv->merge_ok && kv->mstate && !lengths && batch == 1 && nq == 1 &&
+                     plan.gh == 1 && plan.ncb == 1 && plan.nwh == 8 && decode_merge_enabled() &&
+                     ws_bytes >= merge_workspace_bytes(G, a.max_chunks);
+  if (merge) {
+    a.mcnt = (int*)kv->mstate;
+    a.xo = (float*)((char*)kv->mstate + merge_counter_bytes(G));
+    a.xml = a.xo + (size_t)G * 8 * 8 * D;
+    a.gate = gate;
+    a.gate32 = proj ? proj->q_proj : nullptr;
+    a.out = out;
+  }
   mi_status st;
   if (proj) {
     if (nq != 1 || batch != 1) return mi::fail(MI_ERR_INVALID_ARG, "projection input: one token");
@@ -925,6 +1159,7 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
   else
     st = launch_split<8, 1, 1>(a, batch, stream);
   MI_TRY(st);
+  if (merge) return MI_OK;  // merged and written by the split launch
   CombineArgs c;
   c.offsets = offsets;
   c.lengths = lengths;
@@ -974,7 +1209,7 @@ mi_status cache_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float
   for (int32_t t0 = 0; t0 < n; t0 += 4) {
     const int nq = (n - t0) < 4 ? (n - t0) : 4;
     const SplitPlan plan = plan_split(past_pos + t0 + nq, 1, kv->G, nq);
-    need = std::max(need, split_workspace_bytes(1, kv->G, plan.max_chunks, nq));
+    need = std::max(need, attend_workspace_bytes(kv->G, plan.max_chunks, nq));
   }
   void* ws;
   MI_TRY(mi::kv_workspace(kv, need, stream, &ws));
@@ -991,14 +1226,50 @@ mi_status cache_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float
     }
     MI_TRY(run_split(kv->k[layer], kv->v[layer], nullptr, nullptr, rows, lim0 + t0,
                      rows, 1, kv->H, kv->G, nq, q + qoff, gate ? gate + qoff : nullptr,
-                     out + qoff, ws, kv->ws_bytes, stream, app));
+                     out + qoff, ws, kv->ws_bytes, stream, app, nullptr, kv));
   }
   return MI_OK;
 }
 
 }  // namespace
 
+namespace {
+// Records the XCD each workgroup runs on (HW_REG_XCC_ID).
+__global__ void xcc_probe_kernel(int* out) {
+  if (threadIdx.x == 0) {
+    int v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(v));
+    out[blockIdx.x] = v;
+  }
+}
+}  // namespace
+
 namespace mi {
+size_t merge_state_bytes(int G) {
+  return merge_counter_bytes(G) + (size_t)G * 8 * (8 * D + 64) * sizeof(float);
+}
+
+bool xcd_round_robin() {
+  static std::atomic<int> known[64];  // per device: 0 unknown, 1 yes, 2 no
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  const int k = known[dev].load(std::memory_order_acquire);
+  if (k) return k == 1;
+  constexpr int kN = 2048;
+  int* d = nullptr;
+  bool ok = hipMalloc(&d, kN * sizeof(int)) == hipSuccess;
+  std::vector<int> h(kN, -1);
+  if (ok) {
+    hipLaunchKernelGGL(xcc_probe_kernel, dim3(kN), dim3(64), 0, 0, d);
+    ok = hipGetLastError() == hipSuccess &&
+         hipMemcpy(h.data(), d, kN * sizeof(int), hipMemcpyDeviceToHost) == hipSuccess;
+  }
+  if (d) (void)hipFree(d);
+  for (int b = 0; ok && b < kN; b++) ok = h[b] == b % 8;
+  known[dev].store(ok ? 1 : 2, std::memory_order_release);
+  return ok;
+}
+
 mi_status attend_cache(mi_kv* kv, int32_t layer, const _Float16* q, const _Float16* gate,
                        _Float16* out, int64_t past_pos, int32_t n, hipStream_t stream) {
   return cache_attend(kv, layer, q, gate, out, past_pos, n, stream);
@@ -1122,13 +1393,13 @@ extern "C" mi_status mi_attn_step_proj(mi_kv* kv, int32_t layer, const float* q_
   const int64_t rows = pos + 1;
   const SplitPlan plan = plan_split(rows, 1, kv->G, 1);
   void* ws;
-  MI_TRY(mi::kv_workspace(kv, split_workspace_bytes(1, kv->G, plan.max_chunks, 1), (hipStream_t)stream, &ws));
+  MI_TRY(mi::kv_workspace(kv, attend_workspace_bytes(kv->G, plan.max_chunks, 1), (hipStream_t)stream, &ws));
   AppendRows app;
   app.row0 = pos;
   app.n = 1;
   MI_TRY(run_split(kv->k[layer], kv->v[layer], nullptr, nullptr, rows, rows, rows, 1, kv->H,
                    kv->G, 1, nullptr, nullptr, (_Float16*)out, ws, kv->ws_bytes,
-                   (hipStream_t)stream, app, &x));
+                   (hipStream_t)stream, app, &x, kv));
   kv->len[layer] = pos + 1;
   return MI_OK;
 }

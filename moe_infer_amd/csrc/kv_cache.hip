@@ -297,6 +297,15 @@ extern "C" mi_status mi_kv_create(int32_t num_layers, int32_t num_q_heads,
     delete kv;
     return st;
   }
+  // the in-launch merge state (its counters must start at zero)
+  hipError_t e = hipMalloc(&kv->mstate, mi::merge_state_bytes(kv->G));
+  if (e == hipSuccess) e = hipMemset(kv->mstate, 0, mi::merge_state_bytes(kv->G));
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    mi_kv_destroy(kv);
+    return mi::hip_status(e, "in-launch merge state");
+  }
+  kv->merge_ok = mi::xcd_round_robin();
   *out = kv;
   return MI_OK;
 }
@@ -306,6 +315,7 @@ extern "C" void mi_kv_destroy(mi_kv* kv) {
   (void)hipDeviceSynchronize();
   free_layers(kv);
   if (kv->ws) (void)hipFree(kv->ws);
+  if (kv->mstate) (void)hipFree(kv->mstate);
   for (void* p : kv->ws_retired) (void)hipFree(p);
   delete kv;
 }
