@@ -1011,18 +1011,53 @@ attn_prefill64_kernel(PrefillArgs a) {
   }
   if (pending) pv(nt - 1);
 
-  // Merge of the two key halves: wave (qb, kp) hands column block 1 - kp to
-  // its partner through LDS and finishes block kp.  Region (qb, b) holds
-  // 32 KiB of O^T (lane-contiguous 16-byte pieces) and the (m, l) pairs.
-  // Both blocks are named at compile time (a run-time block index would
-  // turn every accumulator access into a select).
+  // Merge of the two key halves: wave (qb, kp) finishes query half kp of
+  // rows qb (column block kp) and hands the other block to its partner
+  // through LDS.  The wave of key half 1 first swaps its two blocks (and
+  // their (m, l)), so that from here on block 0 is the one finished and
+  // block 1 the one handed over in every wave: the code below names fixed
+  // accumulation registers (a block index that differed by wave would turn
+  // every accumulator access into a select, and a block named at compile
+  // time in two copies of this code left the compiler copying all 256 out
+  // of the accumulation registers, with spills).  Region (qb, h) holds
+  // 32 KiB of O^T of query half h (lane-contiguous 16-byte pieces) and the
+  // (m, l) pairs.  Every long-latency access
+  // of the epilogue is issued in one batch: the gate rows before the
+  // hand-over (their global latency overlaps it), the partner's 32 pieces
+  // in two batches of 16 right after it (in registers Q^T held), so that no
+  // access waits for the one before it.
   __syncthreads();  // every wave is done with the K/V tiles
+  if (__builtin_amdgcn_readfirstlane(kp)) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const f32x16 t = acc[0][i];
+      acc[0][i] = acc[1][i];
+      acc[1][i] = t;
+    }
+    const float tm = m[0], tl = l[0];
+    m[0] = m[1]; l[0] = l[1]; m[1] = tm; l[1] = tl;
+  }
   float* const rgn = (float*)lds;                   // [2][2][8*4][64][4]
   float* const mlr = rgn + 2 * 2 * 8 * 4 * 64 * 4;  // [2][2][32][2]
-  auto finish = [&](auto OB) {
-    constexpr int ob = decltype(OB)::value;  // the block this wave finishes
-    constexpr int gb = 1 - ob;               // the block it hands over
-    float* dst = rgn + (qb * 2 + gb) * (8 * 4 * 64 * 4);
+  auto finish = [&](auto GATED) {
+    constexpr int ob = 0, gb = 1;
+    constexpr bool gated = decltype(GATED)::value;
+    const int qo = q0 + 64 * qb + 32 * kp + col;
+    const bool qvalid = qo < a.n;
+    // Output: lane (col, hl) holds columns 32 i + 8 g + 4 hl .. + 3 of
+    // query qo; a v_permlane32_swap between the two lane halves gives lane
+    // hl all eight columns of chunk (i, g = 2 j + hl), so every lane writes
+    // whole 16-byte chunks (half the store instructions of 8-byte pieces).
+    _Float16* op = a.out + ((int64_t)qo * a.H + hq) * D;
+    f16x8 gv[16];
+    if constexpr (gated) {
+      const _Float16* gp = a.gate + ((int64_t)(qvalid ? qo : 0) * a.H + hq) * D;
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) gv[2 * i + j] = *(const f16x8*)(gp + 32 * i + 8 * (2 * j + hl));
+    }
+    float* dst = rgn + (qb * 2 + 1 - kp) * (8 * 4 * 64 * 4);
 #pragma unroll
     for (int i = 0; i < 8; i++)
 #pragma unroll
@@ -1032,77 +1067,72 @@ attn_prefill64_kernel(PrefillArgs a) {
         *(f32x4*)(dst + ((i * 4 + e4) * 64 + lane) * 4) = o;
       }
     if (hl == 0) {
-      float* mdst = mlr + ((qb * 2 + gb) * 32 + col) * 2;
+      float* mdst = mlr + ((qb * 2 + 1 - kp) * 32 + col) * 2;
       mdst[0] = m[gb];
       mdst[1] = l[gb];
     }
-    const int qo = q0 + 64 * qb + 32 * ob + col;
-    const bool qvalid = qo < a.n;
     mi::sync_lds();
-    const float* src = rgn + (qb * 2 + ob) * (8 * 4 * 64 * 4);
-    const float* msrc = mlr + ((qb * 2 + ob) * 32 + col) * 2;
+    const float* src = rgn + (qb * 2 + kp) * (8 * 4 * 64 * 4);
+    const float* msrc = mlr + ((qb * 2 + kp) * 32 + col) * 2;
     const float mo = msrc[0], lo = msrc[1];
     const float M = fmaxf(m[ob], mo);
     const float sw = __builtin_amdgcn_exp2f(m[ob] - M), so = __builtin_amdgcn_exp2f(mo - M);
     const float L = l[ob] * sw + lo * so;
     const float inv = (L > 0.f) ? 1.f / L : 0.f;
     const float fw = sw * inv, fo = so * inv;
-    // Output: lane (col, hl) holds columns 32 i + 8 g + 4 hl .. + 3 of
-    // query qo; a v_permlane32_swap between the two lane halves gives lane
-    // hl all eight columns of chunk (i, g = 2 j + hl), so every lane writes
-    // whole 16-byte chunks (half the store instructions of 8-byte pieces).
-    _Float16* op = a.out + ((int64_t)qo * a.H + hq) * D;
-    const _Float16* gp = a.gate ? a.gate + ((int64_t)(qvalid ? qo : 0) * a.H + hq) * D : nullptr;
     auto swap32 = [](float& lo, float& hi) {  // lo of the upper half <-> hi of the lower half
       auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
       lo = __uint_as_float(r[0]);
       hi = __uint_as_float(r[1]);
     };
-    auto store = [&](auto GATED) {
+    // the partner's pieces in two batches of 16 (64 registers each)
+    f32x4 x[16];
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
+    for (int i = 0; i < 8; i++) {
+      if (i % 4 == 0) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-          // y[k][e]: value e of chunk (i, 2 j + k) held by this lane
-          float y[2][4];
-#pragma unroll
-          for (int k = 0; k < 2; k++) {
-            const int g4 = 2 * j + k;
-            const f32x4 x = *(const f32x4*)(src + ((i * 4 + g4) * 64 + lane) * 4);
-#pragma unroll
-            for (int e = 0; e < 4; e++) y[k][e] = acc[ob][i][4 * g4 + e] * fw + x[e] * fo;
-          }
-          // lane half 0 keeps chunk 2j (its columns 0..3, receives 4..7);
-          // lane half 1 keeps chunk 2j + 1 (receives 0..3, its 4..7)
-#pragma unroll
-          for (int e = 0; e < 4; e++) swap32(y[0][e], y[1][e]);
-          // now lane half 0: y[0] = columns 0..3, y[1] = 4..7 of chunk 2j;
-          // lane half 1: y[0] = columns 0..3, y[1] = 4..7 of chunk 2j + 1
-          const int cofs = 32 * i + 8 * (2 * j + hl);
-          f16x8 h;
-          if constexpr (decltype(GATED)::value) {
-            const f16x8 g = *(const f16x8*)(gp + cofs);
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-              h[e] = (_Float16)mi::gate_mul(y[0][e], (float)g[e]);
-              h[4 + e] = (_Float16)mi::gate_mul(y[1][e], (float)g[4 + e]);
-            }
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-              h[e] = (_Float16)y[0][e];
-              h[4 + e] = (_Float16)y[1][e];
-            }
-          }
-          if (qvalid) *(f16x8*)(op + cofs) = h;
-        }
+        for (int p = 0; p < 16; p++) x[p] = *(const f32x4*)(src + ((i * 4 + p) * 64 + lane) * 4);
       }
-    };
-    if (a.gate) store(std::true_type{});
-    else store(std::false_type{});
+      // one column chunk at a time (keeps the accumulator copies short-lived)
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        // y[k][e]: value e of chunk (i, 2 j + k) held by this lane
+        float y[2][4];
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+          const int g4 = 2 * j + k;
+#pragma unroll
+          for (int e = 0; e < 4; e++) y[k][e] = acc[ob][i][4 * g4 + e] * fw + x[(i % 4) * 4 + g4][e] * fo;
+        }
+        // lane half 0 keeps chunk 2j (its columns 0..3, receives 4..7);
+        // lane half 1 keeps chunk 2j + 1 (receives 0..3, its 4..7)
+#pragma unroll
+        for (int e = 0; e < 4; e++) swap32(y[0][e], y[1][e]);
+        // now lane half 0: y[0] = columns 0..3, y[1] = 4..7 of chunk 2j;
+        // lane half 1: y[0] = columns 0..3, y[1] = 4..7 of chunk 2j + 1
+        const int cofs = 32 * i + 8 * (2 * j + hl);
+        f16x8 h;
+        if constexpr (gated) {
+          const f16x8 g = gv[2 * i + j];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            h[e] = (_Float16)mi::gate_mul(y[0][e], (float)g[e]);
+            h[4 + e] = (_Float16)mi::gate_mul(y[1][e], (float)g[4 + e]);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            h[e] = (_Float16)y[0][e];
+            h[4 + e] = (_Float16)y[1][e];
+          }
+        }
+        if (qvalid) *(f16x8*)(op + cofs) = h;
+      }
+    }
   };
-  if (kp == 0) finish(std::integral_constant<int, 0>{});
-  else finish(std::integral_constant<int, 1>{});
+  if (a.gate) finish(std::true_type{});
+  else finish(std::false_type{});
 }
 
 // Queries per wave of the prefill kernel: 64 (attn_prefill64_kernel, the
