@@ -59,7 +59,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="bounded CPU-baseline sample length")
-    p.add_argument("--only", default="", help="comma list of decode,prefill,verify,ragged,oproj")
+    p.add_argument("--only", default="", help="comma list of decode,prefill,verify,ragged,oproj,ceiling")
     p.add_argument("--copy-calib", action="store_true",
                    help="also run a plain 256 MiB device copy (reference for HBM counters)")
     return p.parse_args()
@@ -395,6 +395,49 @@ def main():
               file=sys.stderr, flush=True)
         del wb, wq
 
+    # ------------------------------------------------------------- MFMA ceiling
+    # What the MFMA units reach on this part with nothing else in the loop:
+    # one wave per SIMD on every CU, back-to-back v_mfma_f32_32x32x16_f16,
+    # random N(0,1) operands and then zero operands (the data's share of the
+    # power).  The prefill's fraction of nominal peak is read against this.
+    if not only or "ceiling" in only:
+        import ctypes as C
+        wgs, iters = 256, 2048
+        ops = randn(256 * 12 * 8, seed=51)
+        cout = torch.empty(wgs * 256, dtype=torch.float32, device=dev)
+        clk = torch.zeros(2 * wgs, dtype=torch.int64, device=dev)
+        stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        flop = wgs * 4 * iters * 8 * 32768
+        ceil = {"workgroups": wgs, "waves_per_simd": 1, "mfma": "v_mfma_f32_32x32x16_f16",
+                "flop_per_launch": flop}
+        for name, o in (("random", ops), ("zero", torch.zeros_like(ops))):
+            def launch():
+                _lib.check(_lib.lib().mi_bench_mfma_ceiling(
+                    C.c_void_p(o.data_ptr()), iters, wgs, C.c_void_p(cout.data_ptr()),
+                    C.c_void_p(clk.data_ptr()), stream))
+            for _ in range(5):
+                launch()
+            torch.cuda.synchronize()
+            _lib.prof_enable(True)
+            for _ in range(10):
+                launch()
+            torch.cuda.synchronize()
+            us, _ = _lib.prof_read("mfma_ceiling")
+            _lib.prof_enable(False)
+            c = clk.cpu().numpy().reshape(wgs, 2).astype(np.float64)
+            mhz = float(np.median(c[:, 0] / c[:, 1] * 100.0))
+            tf = flop / (us * 1e-6) / 1e12
+            ceil[name] = {"kernel_us": us, "tflops": tf, "frac_of_peak": tf / f16_peak,
+                          "clock_mhz": mhz,
+                          # clocks per MFMA per SIMD: 32 is full issue
+                          "clk_per_mfma": float(np.median(c[:, 0])) / (iters * 8)}
+        rec["mfma_ceiling"] = ceil
+        print(f"[bench] mfma ceiling random {ceil['random']['tflops']:.0f} TFLOP/s "
+              f"({ceil['random']['frac_of_peak']:.3f} of peak, {ceil['random']['clock_mhz']:.0f} MHz, "
+              f"{ceil['random']['clk_per_mfma']:.1f} clk/MFMA); zero operands "
+              f"{ceil['zero']['tflops']:.0f} TFLOP/s ({ceil['zero']['clock_mhz']:.0f} MHz)",
+              file=sys.stderr, flush=True)
+
     # -------------------------------------------------------------- CPU baseline
     # The reference's CPU attention (src/math_util.rs:264-269, 323-383, one
     # thread as cpu.rs:149-163 runs it) on f32 inputs widened once outside
@@ -490,6 +533,15 @@ def main():
                                     "traffic_source": traffic_src}
         line["prefill"] = {k2: (round(v2, 3) if isinstance(v2, float) else v2)
                            for k2, v2 in p.items()}
+        mc = rec.get("mfma_ceiling")
+        if mc:
+            # the same kernel time against what MFMA alone reaches on this part
+            line["roofline_prefill"]["frac_of_mfma_ceiling"] = round(
+                p["tflops_kernel"] / mc["random"]["tflops"], 4)
+    if "mfma_ceiling" in rec:
+        line["mfma_ceiling"] = {k2: ({k3: round(v3, 3) for k3, v3 in v2.items()}
+                                     if isinstance(v2, dict) else v2)
+                                for k2, v2 in rec["mfma_ceiling"].items()}
     vr = rec.get("verify")
     if vr:
         ach = C5_BYTES / (vr["split_kernel_us"] * 1e3)

@@ -330,6 +330,20 @@ mi_status mi_matvec_q4(const mi_f16* x, const uint32_t* w_packed,
 void mi_prof_enable(int on);
 mi_status mi_prof_read(const char* kernel, double* avg_us, int64_t* count);
 
+/* MFMA issue ceiling (measurement only; no counterpart in the reference):
+ * `workgroups` workgroups of 4 waves, one wave per SIMD, each issuing
+ * `iters` x 8 v_mfma_f32_32x32x16_f16 back to back (4 independent chains,
+ * A rotating over 8 register fragments, no LDS / VALU / memory in the loop).
+ * `operands` holds (8 + 4) x 8 halves per thread of a workgroup (256
+ * threads, 24 KiB; all workgroups read the same ones); `out` receives one
+ * float per thread (workgroups x 256) so nothing is optimised away;
+ * `clocks` receives per workgroup the shader-clock cycles and the 100 MHz
+ * reference-clock ticks of its loop.  bench.py prices the prefill against
+ * what this reaches with random and with zero operands.  Kernel name for
+ * mi_prof_read: "mfma_ceiling". */
+mi_status mi_bench_mfma_ceiling(const mi_f16* operands, int32_t iters, int32_t workgroups,
+                                float* out, uint64_t* clocks, mi_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -65,6 +65,7 @@ SIGNATURES = [
     ("mi_matvec_q4", ST, [P, P, P, P, I32, P, I32, I32, P]),
     ("mi_prof_enable", None, [C.c_int]),
     ("mi_prof_read", ST, [C.c_char_p, C.POINTER(C.c_double), C.POINTER(I64)]),
+    ("mi_bench_mfma_ceiling", ST, [P, I32, I32, P, P, P]),
 ]
 
 
