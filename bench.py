@@ -224,6 +224,30 @@ def main():
                          backlog_ms=args.steps * LAYERS * 0.25 + 20)
         _lib.prof_enable(False)
         del graph
+        # The step followed by the layer's o_proj (bf16 2048 x 4096 per layer,
+        # 10 x 16 MiB of weights) as the engine issues them: mi_attn_step,
+        # then mi_matvec_bf16 of its output.
+        od = 2048
+        wos = [(randn(od, H * D, seed=1400 + i).float() * 0.05).to(torch.bfloat16)
+               for i in range(LAYERS)]
+        ys = [torch.empty(od, dtype=torch.float32, device=dev) for _ in range(LAYERS)]
+
+        def step_then_oproj():
+            for layer in range(LAYERS):
+                mi.attn_step(cache, layer, qs[layer], kn[layer], vn[layer], pos, gate=gs[layer],
+                             out=outs[layer])
+                mi.matvec_bf16(outs[layer], wos[layer], out=ys[layer])
+
+        ms_sep = timed(step_then_oproj, args.steps, args.warmup,
+                       backlog_ms=args.steps * LAYERS * 0.3 + 20)
+        sep_mv_us, _ = _lib.prof_read("matvec_bf16")
+        _lib.prof_enable(False)
+        del wos
+        oproj_rec = {"us_per_layer": ms_sep * 1000 / LAYERS, "matvec_kernel_us": sep_mv_us,
+                     "shape": [od, H * D],
+                     "bytes_per_layer": C2_BYTES + od * H * D * 2 + od * 4}
+        print(f"[bench] decode step + o_proj {ms_sep * 100:.2f} us/layer "
+              f"(matvec kernel {sep_mv_us:.2f})", file=sys.stderr, flush=True)
         us_layer = ms * 1000 / LAYERS
         rec["decode"] = {
             "proj_step_us_per_layer": ms_proj * 1000 / LAYERS,
@@ -235,6 +259,7 @@ def main():
             "bytes_per_layer": C2_BYTES, "ms_per_step": ms,
             "graph_step_us_per_layer": ms_graph * 1000 / LAYERS,
             "graph_gbps": C2_BYTES / (ms_graph * 1e6 / LAYERS), "graph_matches_eager": graph_ok,
+            "with_oproj": oproj_rec,
         }
         # Attend-only calls at other context lengths (the split plan depends on
         # the length), over 4 layers of 50000 rows (more than the last-level cache).
