@@ -77,6 +77,36 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
 }
 
+// blockIdx -> (KV head, head in group, query tile), heaviest query tile
+// first.  Dispatch is round-robin over the 8 XCDs (bid % 8), and the eight
+// query heads of one (query tile, KV head) go to one XCD, so that their
+// identical K/V tile reads share its L2.  With two KV heads, XCDs 0-3 take
+// KV head 0 and XCDs 4-7 KV head 1, so an XCD's L2 holds one head's K/V
+// (4 MiB at 4096 rows) rather than both; the query tiles of a KV head are
+// dealt to its four XCDs in a snake (block j of 4 tiles: XCD i takes tile
+// rank 4j + i for even j, 4j + 3 - i for odd j), which gives every XCD the
+// same causal work.  Other head counts deal (query tile, KV head) groups
+// over all 8 XCDs in the same snake.  The grid is (8 heads x ntiles x G)
+// rounded up to 64 workgroups; returns false for its padding.
+__device__ __forceinline__ bool prefill_item(int bid, const PrefillArgs& a, int& kvh, int& hg,
+                                             int& qtile) {
+  const int xcd = bid & 7, r = bid >> 3;
+  hg = r & 7;
+  const int jb = r >> 3;
+  int rank;
+  if (a.G == 2) {
+    const int xi = xcd & 3;
+    kvh = xcd >> 2;
+    rank = 4 * jb + ((jb & 1) ? 3 - xi : xi);
+  } else {
+    const int grp = 8 * jb + ((jb & 1) ? 7 - xcd : xcd);
+    kvh = grp % a.G;
+    rank = grp / a.G;
+  }
+  qtile = a.ntiles - 1 - rank;
+  return rank < a.ntiles;
+}
+
 __global__ void __launch_bounds__(256, 1)
 attn_prefill_kernel(PrefillArgs a) {
   extern __shared__ _Float16 lds[];
@@ -85,22 +115,8 @@ attn_prefill_kernel(PrefillArgs a) {
   const int hl = lane >> 5;   // lane half
   const int col = lane & 31;  // query column of this lane
 
-  // blockIdx -> (query tile, KV head, head in group).  Work item li = 8g + h:
-  // group g = (query tile, KV head), heaviest first, h = one of its 8 query
-  // heads.  Dispatch is round-robin over the 8 XCDs (bid % 8), so the 8 heads
-  // of a group go to one XCD and share its L2.  Groups are dealt to the XCDs
-  // in a snake (block j of 8 groups: XCD x takes group 8j + x for even j,
-  // 8j + 7 - x for odd j), so every XCD gets the same causal work; within an
-  // XCD its groups still come heaviest first.
-  const int bid = blockIdx.x;
-  const int xcd = bid & 7, r = bid >> 3;
-  const int jb = r >> 3;
-  const int li = (8 * jb + ((jb & 1) ? 7 - xcd : xcd)) * 8 + (r & 7);
-  if (li >= a.work) return;
-  const int hg = li & 7;
-  const int kvh = (li >> 3) % a.G;
-  const int tile_rank = (li >> 3) / a.G;
-  const int qtile = a.ntiles - 1 - tile_rank;  // heaviest first
+  int kvh, hg, qtile;
+  if (!prefill_item(blockIdx.x, a, kvh, hg, qtile)) return;
   const int hq = kvh * 8 + hg;
   const int q0 = qtile * BQ;
 
@@ -527,15 +543,8 @@ attn_prefill64_kernel(PrefillArgs a) {
   const int hl = lane >> 5;
   const int col = lane & 31;
 
-  const int bid = blockIdx.x;
-  const int xcd = bid & 7, r = bid >> 3;
-  const int jb = r >> 3;
-  const int li = (8 * jb + ((jb & 1) ? 7 - xcd : xcd)) * 8 + (r & 7);
-  if (li >= a.work) return;
-  const int hg = li & 7;
-  const int kvh = (li >> 3) % a.G;
-  const int tile_rank = (li >> 3) / a.G;
-  const int qtile = a.ntiles - 1 - tile_rank;
+  int kvh, hg, qtile;
+  if (!prefill_item(blockIdx.x, a, kvh, hg, qtile)) return;
   const int hq = kvh * 8 + hg;
   const int q0 = qtile * BQ;
 
