@@ -80,15 +80,16 @@ struct SplitArgs {
   _Float16* out;
 };
 
-// Partials are consumed once, by the combine kernel: streaming stores
-// (MI_ATTN_TEMPORAL_PARTIALS at build time keeps the default policy).
-template <typename T>
-__device__ __forceinline__ void store_part(T v, T* p) {
-#if defined(MI_ATTN_TEMPORAL_PARTIALS)
-  *p = v;
-#else
-  __builtin_nontemporal_store(v, p);
-#endif
+// Partials are consumed once, by the combine kernel, on any XCD: written
+// through to memory (sc0 sc1), so that the end of the split launch has no
+// dirty partial lines to write back from the L2s.  Measured at C2 against
+// streaming (nontemporal) and default stores, in one process: 19.87-19.91
+// against 20.12-20.15 us per step.
+__device__ __forceinline__ void store_part(float v, float* p) {
+  asm volatile("global_store_dword %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_part(f32x4 v, f32x4* p) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
 }
 
 // 16-byte streaming load of K/V: read once per launch, so it is not kept in
