@@ -61,3 +61,7 @@ def test_host_side_errors_without_gpu():
     assert b"65535" in lib.mi_last_error()
     with pytest.raises(_lib.MiValueError):
         _lib.check(lib.mi_kv_set_pos(None, 0))
+    # the MFMA ceiling probe checks its arguments before launching
+    assert lib.mi_bench_mfma_ceiling(None, 1, 1, None, None, None) == _lib.MI_ERR_INVALID_ARG
+    assert lib.mi_bench_mfma_ceiling(fake, 0, 1, fake, fake, None) == _lib.MI_ERR_INVALID_ARG
+    assert lib.mi_bench_mfma_ceiling(fake, 1, 0, fake, fake, None) == _lib.MI_ERR_INVALID_ARG
