@@ -88,8 +88,11 @@ struct SplitArgs {
 __device__ __forceinline__ void store_part(float v, float* p) {
   asm volatile("global_store_dword %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
 }
+// A store of more than 64 bits reads its data registers after issue: the
+// next instruction may not overwrite them without wait states, which the
+// compiler inserts for its own stores but not for asm ones, hence the nops.
 __device__ __forceinline__ void store_part(f32x4 v, f32x4* p) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
+  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1\n s_nop 1" ::"v"(p), "v"(v) : "memory");
 }
 
 // 16-byte streaming load of K/V: read once per launch, so it is not kept in
@@ -226,46 +229,29 @@ struct HeadPart {
 // added 1.9 us to a launch of 256 workgroups, but after a real C2 split the
 // chain takes ~5 us, as long as the combine launch.
 
-// Loads without waiting (the caller waits, see wait_regs).  Within the XCD
-// a plain load: it misses this CU's L1 (which never held those lines in this
-// launch; L1 and L2 are invalidated at every kernel start) and hits the
-// XCD's L2, where the members' stores landed.  Across XCDs sc0 sc1 (the
-// data was written through to memory).
-__device__ __forceinline__ f32x4 ld_xcd4(const float* p) {
-  f32x4 v;
-  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
-  return v;
-}
-__device__ __forceinline__ float ld_xcd1(const float* p) {
-  float v;
-  asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p) : "memory");
-  return v;
+// Loads the compiler tracks (it places the waits itself: an asm load whose
+// result the compiler copied before a separate wait would copy stale
+// data).  Within the XCD a plain load: it misses this CU's L1 (which never
+// held those lines in this launch; L1 is invalidated at every kernel start)
+// and hits the XCD's L2, where the members' stores landed; the barrier
+// before the loads keeps them after the arrival count.  Across XCDs,
+// system-scope atomic loads (sc0 sc1: past this XCD's L2, from memory, where
+// the data was written through).
+__device__ __forceinline__ f32x4 ld_xcd4(const float* p) { return *(const f32x4*)p; }
+__device__ __forceinline__ float ld_xcd1(const float* p) { return *p; }
+__device__ __forceinline__ float ld_dev1(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 __device__ __forceinline__ f32x4 ld_dev4(const float* p) {
-  f32x4 v;
-  asm volatile("global_load_dwordx4 %0, %1, off sc0 sc1" : "=v"(v) : "v"(p) : "memory");
-  return v;
-}
-__device__ __forceinline__ float ld_dev1(const float* p) {
-  float v;
-  asm volatile("global_load_dword %0, %1, off sc0 sc1" : "=v"(v) : "v"(p) : "memory");
-  return v;
+  return f32x4{ld_dev1(p), ld_dev1(p + 1), ld_dev1(p + 2), ld_dev1(p + 3)};
 }
 __device__ __forceinline__ void st_dev4(float* p, f32x4 v) {  // written through to memory
-  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
+  // (the nops: as for store_part, the data registers are read after issue)
+  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1\n s_nop 1" ::"v"(p), "v"(v) : "memory");
 }
 __device__ __forceinline__ void st_dev1(float* p, float v) {
   asm volatile("global_store_dword %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
 }
-// Waits for this thread's outstanding loads; the empty asm statements make
-// every later use of the loaded registers follow the wait.
-template <int N>
-__device__ __forceinline__ void wait_regs(f32x4 (&o)[N], float (&m)[N], float (&l)[N]) {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma unroll
-  for (int i = 0; i < N; i++) asm volatile("" : "+v"(o[i]), "+v"(m[i]), "+v"(l[i]));
-}
-
 constexpr int kMergeStride = 64;  // ints between counters (256 bytes)
 
 template <int NT>
@@ -305,7 +291,6 @@ __device__ void merge_tail(const SplitArgs& a) {
       m[u] = ld_xcd1(a.part_ml + slot * 64 + 2 * col);
       l[u] = ld_xcd1(a.part_ml + slot * 64 + 2 * col + 1);
     }
-    wait_regs(o, m, l);
     float mb = M;
 #pragma unroll
     for (int u = 0; u < 16; u++)
@@ -350,7 +335,6 @@ __device__ void merge_tail(const SplitArgs& a) {
     m[xx] = ld_dev1(a.xml + (hy * 8 + xx) * 64 + 2 * col);
     l[xx] = ld_dev1(a.xml + (hy * 8 + xx) * 64 + 2 * col + 1);
   }
-  wait_regs(o, m, l);
   float Mh = kNegBig;
 #pragma unroll
   for (int xx = 0; xx < 8; xx++)
