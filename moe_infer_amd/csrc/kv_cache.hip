@@ -125,6 +125,58 @@ kv_pack_kernel(const _Float16* __restrict__ k, const _Float16* __restrict__ v,
   }
 }
 
+// The same for head_dim 256 with 32-bit item indices (the host checks the
+// item count fits): the row / head / chunk of an item come from shifts and
+// one 32-bit division by G instead of the generic kernel's 64-bit divisions
+// by run-time values, which cost more than the copy's own instructions.
+__global__ void __launch_bounds__(256)
+kv_pack256_kernel(const _Float16* __restrict__ k, const _Float16* __restrict__ v,
+                  _Float16* __restrict__ kblk, _Float16* __restrict__ vblk, int64_t pos,
+                  uint32_t n, uint32_t G, uint32_t nblk) {
+  constexpr int D = mi::kHeadDim;
+  constexpr uint32_t cvec = D / 8;  // 16-byte chunks per head row
+  const uint32_t nk = n * G * cvec;
+  const uint32_t total = nk + nblk * G * cvec;
+  const int64_t b_first = pos / MI_KV_VBLOCK;
+  for (uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += gridDim.x * blockDim.x) {
+    if (idx < nk) {
+      const uint32_t rh = idx / cvec, c = idx % cvec;
+      const uint32_t rr = rh / G, h = rh - rr * G;
+      *(f16x8*)(kblk + mi::k_offset(pos + rr, (int)h, 8 * c, (int)G, D)) =
+          *(const f16x8*)(k + ((int64_t)rr * G + h) * D + 8 * c);
+      continue;
+    }
+    const uint32_t vi = idx - nk;
+    const uint32_t bh = vi / cvec, d0 = (vi % cvec) * 8;
+    const uint32_t bb = bh / G, h = bh - bb * G;
+    const int64_t b = b_first + bb;
+    const int64_t r0 = b * MI_KV_VBLOCK;
+    _Float16* blk = vblk + ((b * G + h) * (int64_t)D + d0) * MI_KV_VBLOCK;
+    if (r0 >= pos && r0 + MI_KV_VBLOCK <= pos + n) {
+      f16x8 rowv[8];
+#pragma unroll
+      for (int rr = 0; rr < 8; rr++)
+        rowv[rr] = *(const f16x8*)(v + ((r0 + rr - pos) * G + h) * D + d0);
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        f16x8 col;
+#pragma unroll
+        for (int rr = 0; rr < 8; rr++) col[rr] = rowv[rr][i];
+        *(f16x8*)(blk + i * MI_KV_VBLOCK) = col;
+      }
+    } else {
+      for (int rr = 0; rr < 8; rr++) {
+        const int64_t r = r0 + rr;
+        if (r < pos || r >= pos + n) continue;
+        const f16x8 row = *(const f16x8*)(v + ((r - pos) * G + h) * D + d0);
+#pragma unroll
+        for (int i = 0; i < 8; i++) blk[i * MI_KV_VBLOCK + rr] = row[i];
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------- host helpers --
 
 namespace {
@@ -261,6 +313,11 @@ mi_status kv_pack_rows(const _Float16* k, const _Float16* v, _Float16* dst_k, _F
   const int64_t nblk = (pos + n - 1) / MI_KV_VBLOCK - pos / MI_KV_VBLOCK + 1;
   const int64_t items = (n + nblk) * G * (D / 8);
   const int grid = (int)std::min<int64_t>((items + 255) / 256, 4096);
+  if (D == kHeadDim && items + (int64_t)grid * 256 < ((int64_t)1 << 32)) {
+    MI_HIP(mi::launch("kv_pack", kv_pack256_kernel, dim3(grid), dim3(256), 0, stream, k, v, dst_k,
+                      dst_v, pos, (uint32_t)n, (uint32_t)G, (uint32_t)nblk));
+    return MI_OK;
+  }
   MI_HIP(mi::launch("kv_pack", kv_pack_kernel, dim3(grid), dim3(256), 0, stream, k, v, dst_k,
                     dst_v, pos, n, G, D));
   return MI_OK;
