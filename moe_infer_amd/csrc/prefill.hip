@@ -642,171 +642,180 @@ attn_prefill64_kernel(PrefillArgs a) {
   };
 
   // S^T = K . Q^T of this wave's 32-key half of tile t for both column
-  // blocks, with the copies of K(tk) (into tile t + 1's buffer) and V(t): one asm block of 32 MFMAs
+  // blocks, with the copies of K(tk) (into tile t + 1's buffer) and, when
+  // with_v, of V(t): one asm block of 32 MFMAs
   // (the scores must come out in ordinary registers, the compiler would
   // give every MFMA of the kernel the accumulation-register form), the K
   // fragments read four k-steps ahead through a ring of four, and one copy
-  // piece issued per k-step (K pieces on even steps, V on odd).  ka: LDS
+  // piece issued per k-step (K pieces on even steps, V on odd).  Only the
+  // first tile takes its V copies here; in the steady walk they go into the
+  // PV phase (copy_v_piece), so that QK's LDS port carries the K fragment
+  // reads and the K copies alone.  ka: LDS
   // byte address of the lane's K fragment 0; mk / mv: LDS byte addresses of
   // the wave's first K / V piece; vk / vv: the lane's byte offsets in the
   // source tiles; sv: offset of the wave's second group of four V pieces.
   // Ends with 16 wait states, since VALU code reads the results next.
   // (m0 in the clobber list: the compiler sets m0 right before each of its
   // own LDS copies, so nothing it holds there lives across the block.)
+  // The asm text is a macro; VC(m0 offset, soffset instruction) stands for
+  // the copy of one V piece, or for nothing.
+#define PF_VCOPY(mo, soi) "s_add_u32 m0, %[mv], " #mo "\n" soi "s_nop 0\n" \
+  "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
+#define PF_NOCOPY(mo, soi)
+#define PF_QK_ASM(VC) \
+    "ds_read_b128 %[r0], %[ka] offset:0\n" \
+    "ds_read_b128 %[r1], %[ka] offset:512\n" \
+    "ds_read_b128 %[r2], %[ka] offset:1024\n" \
+    "ds_read_b128 %[r3], %[ka] offset:1536\n" \
+    "s_waitcnt lgkmcnt(3)\n" \
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r0], %[q0_0], 0\n" \
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r0], %[q1_0], 0\n" \
+    "ds_read_b128 %[r0], %[ka] offset:2048\n" \
+    "s_add_u32 m0, %[mk], 0\n" \
+    "s_mov_b32 %[so], 0\n" \
+    "s_nop 0\n" \
+    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n" \
+    "s_waitcnt lgkmcnt(3)\n" \
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r1], %[q0_1], %[c0]\n" \
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r1], %[q1_1], %[c1]\n" \
+    "ds_read_b128 %[r1], %[ka] offset:2560\n" \
+    VC(0, "s_mov_b32 %[so], 0\n") \
+    "s_waitcnt lgkmcnt(3)\n" \
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r2], %[q0_2], %[c0]\n" \
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r2], %[q1_2], %[c1]\n" \
+    "ds_read_b128 %[r2], %[ka] offset:3072\n" \
+    "s_add_u32 m0, %[mk], 1024\n" \
+    "s_movk_i32 %[so], 1024\n" \
+    "s_nop 0\n" \
+    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n" \
+    "s_waitcnt lgkmcnt(3)\n" \
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r3], %[q0_3], %[c0]\n" \
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r3], %[q1_3], %[c1]\n" \
+    "ds_read_b128 %[r3], %[ka] offset:3584\n" \
+    VC(1024, "s_movk_i32 %[so], 1024\n") \
+    "s_waitcnt lgkmcnt(3)\n" \
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r0], %[q0_4], %[c0]\n" \
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r0], %[q1_4], %[c1]\n" \
+    "ds_read_b128 %[r0], %[ka] offset:4096\n" \
+    "s_add_u32 m0, %[mk], 2048\n" \
+    "s_movk_i32 %[so], 2048\n" \
+    "s_nop 0\n" \
+    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n" \
+    "s_waitcnt lgkmcnt(3)\n" \
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r1], %[q0_5], %[c0]\n" \
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r1], %[q1_5], %[c1]\n" \
+    "ds_read_b128 %[r1], %[ka] offset:4608\n" \
+    VC(2048, "s_movk_i32 %[so], 2048\n") \
+    "s_waitcnt lgkmcnt(3)\n" \
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r2], %[q0_6], %[c0]\n" \
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r2], %[q1_6], %[c1]\n" \
+    "ds_read_b128 %[r2], %[ka] offset:5120\n" \
+    "s_add_u32 m0, %[mk], 3072\n" \
+    "s_movk_i32 %[so], 3072\n" \
+    "s_nop 0\n" \
+    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n" \
+    "s_waitcnt lgkmcnt(3)\n" \
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r3], %[q0_7], %[c0]\n" \
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r3], %[q1_7], %[c1]\n" \
+    "ds_read_b128 %[r3], %[ka] offset:5632\n" \
+    VC(3072, "s_movk_i32 %[so], 3072\n") \
+    "s_waitcnt lgkmcnt(3)\n" \
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r0], %[q0_8], %[c0]\n" \
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r0], %[q1_8], %[c1]\n" \
+    "ds_read_b128 %[r0], %[ka] offset:6144\n" \
+    "s_add_u32 m0, %[mk], 4096\n" \
+    "s_movk_i32 %[so], 4096\n" \
+    "s_nop 0\n" \
+    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n" \
+    "s_waitcnt lgkmcnt(3)\n" \
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r1], %[q0_9], %[c0]\n" \
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r1], %[q1_9], %[c1]\n" \
+    "ds_read_b128 %[r1], %[ka] offset:6656\n" \
+    VC(4096, "s_add_u32 %[so], %[sv], 0\n") \
+    "s_waitcnt lgkmcnt(3)\n" \
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r2], %[q0_10], %[c0]\n" \
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r2], %[q1_10], %[c1]\n" \
+    "ds_read_b128 %[r2], %[ka] offset:7168\n" \
+    "s_add_u32 m0, %[mk], 5120\n" \
+    "s_movk_i32 %[so], 5120\n" \
+    "s_nop 0\n" \
+    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n" \
+    "s_waitcnt lgkmcnt(3)\n" \
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r3], %[q0_11], %[c0]\n" \
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r3], %[q1_11], %[c1]\n" \
+    "ds_read_b128 %[r3], %[ka] offset:7680\n" \
+    VC(5120, "s_add_u32 %[so], %[sv], 1024\n") \
+    "s_waitcnt lgkmcnt(3)\n" \
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r0], %[q0_12], %[c0]\n" \
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r0], %[q1_12], %[c1]\n" \
+    "s_add_u32 m0, %[mk], 6144\n" \
+    "s_movk_i32 %[so], 6144\n" \
+    "s_nop 0\n" \
+    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n" \
+    "s_waitcnt lgkmcnt(2)\n" \
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r1], %[q0_13], %[c0]\n" \
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r1], %[q1_13], %[c1]\n" \
+    VC(6144, "s_add_u32 %[so], %[sv], 2048\n") \
+    "s_waitcnt lgkmcnt(1)\n" \
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r2], %[q0_14], %[c0]\n" \
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r2], %[q1_14], %[c1]\n" \
+    "s_add_u32 m0, %[mk], 7168\n" \
+    "s_movk_i32 %[so], 7168\n" \
+    "s_nop 0\n" \
+    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n" \
+    "s_waitcnt lgkmcnt(0)\n" \
+    "v_mfma_f32_32x32x16_f16 %[c0], %[r3], %[q0_15], %[c0]\n" \
+    "v_mfma_f32_32x32x16_f16 %[c1], %[r3], %[q1_15], %[c1]\n" \
+    VC(7168, "s_add_u32 %[so], %[sv], 3072\n") \
+    "s_nop 15\n"
+#define ASM_OPERANDS \
+  : [c0] "=&v"(c0), [c1] "=&v"(c1), [r0] "=&v"(r0), [r1] "=&v"(r1), [r2] "=&v"(r2), \
+  [r3] "=&v"(r3), [so] "=&s"(so) \
+  : [ka] "v"(ka), [mk] "s"(mk), [mv] "s"(mv), [rk] "s"(rk), [rv] "s"(rv), \
+  [vk] "v"(vk_off), [vv] "v"(vv_off), [sv] "s"(sv_off), \
+  [q0_0] "v"(qf[0][0]), [q0_1] "v"(qf[0][1]), [q0_2] "v"(qf[0][2]), [q0_3] "v"(qf[0][3]), \
+  [q0_4] "v"(qf[0][4]), [q0_5] "v"(qf[0][5]), [q0_6] "v"(qf[0][6]), [q0_7] "v"(qf[0][7]), \
+  [q0_8] "v"(qf[0][8]), [q0_9] "v"(qf[0][9]), [q0_10] "v"(qf[0][10]), [q0_11] "v"(qf[0][11]), \
+  [q0_12] "v"(qf[0][12]), [q0_13] "v"(qf[0][13]), [q0_14] "v"(qf[0][14]), [q0_15] "v"(qf[0][15]), \
+  [q1_0] "v"(qf[1][0]), [q1_1] "v"(qf[1][1]), [q1_2] "v"(qf[1][2]), [q1_3] "v"(qf[1][3]), \
+  [q1_4] "v"(qf[1][4]), [q1_5] "v"(qf[1][5]), [q1_6] "v"(qf[1][6]), [q1_7] "v"(qf[1][7]), \
+  [q1_8] "v"(qf[1][8]), [q1_9] "v"(qf[1][9]), [q1_10] "v"(qf[1][10]), [q1_11] "v"(qf[1][11]), \
+  [q1_12] "v"(qf[1][12]), [q1_13] "v"(qf[1][13]), [q1_14] "v"(qf[1][14]), [q1_15] "v"(qf[1][15]) \
+  : "m0", "memory"
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-  auto qk = [&](int t, int tk, f32x16& c0, f32x16& c1) {
+  auto qk = [&](int t, int tk, f32x16& c0, f32x16& c1, bool with_v) {
     const int ka = lds_addr(kbuf0 + (t & 1) * K_TILE_HALVES + k_lds_off);
     const int mk = __builtin_amdgcn_readfirstlane(k_piece_lds(t + 1));
     const int mv = __builtin_amdgcn_readfirstlane(v_piece_lds(t));
     const __amdgpu_buffer_rsrc_t rk = k_tile_src(tk), rv = v_tile_src(t);
     f16x8 r0, r1, r2, r3;
     int so;
+    if (with_v)
+      asm volatile(PF_QK_ASM(PF_VCOPY) ASM_OPERANDS);
+    else
+      asm volatile(PF_QK_ASM(PF_NOCOPY) ASM_OPERANDS);
+  };
+  // Copy of V piece pi of tile t (the wave's 8 pieces, as in the asm block),
+  // issued in the first eight slots of the PV phase: V(t) lands in the
+  // buffer PV(t-2) read, which the previous iteration's barrier freed, and
+  // the iteration's closing wait covers it.
+  auto copy_v_piece = [&](int t, int pi) {
+    const int mv = __builtin_amdgcn_readfirstlane(v_piece_lds(t)) + 1024 * pi;
+    const int so = pi < 4 ? 1024 * pi : sv_off + 1024 * (pi - 4);
     asm volatile(
-    "ds_read_b128 %[r0], %[ka] offset:0\n"
-    "ds_read_b128 %[r1], %[ka] offset:512\n"
-    "ds_read_b128 %[r2], %[ka] offset:1024\n"
-    "ds_read_b128 %[r3], %[ka] offset:1536\n"
-    "s_waitcnt lgkmcnt(3)\n"
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r0], %[q0_0], 0\n"
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r0], %[q1_0], 0\n"
-    "ds_read_b128 %[r0], %[ka] offset:2048\n"
-    "s_add_u32 m0, %[mk], 0\n"
-    "s_mov_b32 %[so], 0\n"
-    "s_nop 0\n"
-    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n"
-    "s_waitcnt lgkmcnt(3)\n"
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r1], %[q0_1], %[c0]\n"
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r1], %[q1_1], %[c1]\n"
-    "ds_read_b128 %[r1], %[ka] offset:2560\n"
-    "s_add_u32 m0, %[mv], 0\n"
-    "s_mov_b32 %[so], 0\n"
-    "s_nop 0\n"
-    "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
-    "s_waitcnt lgkmcnt(3)\n"
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r2], %[q0_2], %[c0]\n"
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r2], %[q1_2], %[c1]\n"
-    "ds_read_b128 %[r2], %[ka] offset:3072\n"
-    "s_add_u32 m0, %[mk], 1024\n"
-    "s_movk_i32 %[so], 1024\n"
-    "s_nop 0\n"
-    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n"
-    "s_waitcnt lgkmcnt(3)\n"
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r3], %[q0_3], %[c0]\n"
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r3], %[q1_3], %[c1]\n"
-    "ds_read_b128 %[r3], %[ka] offset:3584\n"
-    "s_add_u32 m0, %[mv], 1024\n"
-    "s_movk_i32 %[so], 1024\n"
-    "s_nop 0\n"
-    "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
-    "s_waitcnt lgkmcnt(3)\n"
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r0], %[q0_4], %[c0]\n"
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r0], %[q1_4], %[c1]\n"
-    "ds_read_b128 %[r0], %[ka] offset:4096\n"
-    "s_add_u32 m0, %[mk], 2048\n"
-    "s_movk_i32 %[so], 2048\n"
-    "s_nop 0\n"
-    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n"
-    "s_waitcnt lgkmcnt(3)\n"
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r1], %[q0_5], %[c0]\n"
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r1], %[q1_5], %[c1]\n"
-    "ds_read_b128 %[r1], %[ka] offset:4608\n"
-    "s_add_u32 m0, %[mv], 2048\n"
-    "s_movk_i32 %[so], 2048\n"
-    "s_nop 0\n"
-    "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
-    "s_waitcnt lgkmcnt(3)\n"
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r2], %[q0_6], %[c0]\n"
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r2], %[q1_6], %[c1]\n"
-    "ds_read_b128 %[r2], %[ka] offset:5120\n"
-    "s_add_u32 m0, %[mk], 3072\n"
-    "s_movk_i32 %[so], 3072\n"
-    "s_nop 0\n"
-    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n"
-    "s_waitcnt lgkmcnt(3)\n"
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r3], %[q0_7], %[c0]\n"
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r3], %[q1_7], %[c1]\n"
-    "ds_read_b128 %[r3], %[ka] offset:5632\n"
-    "s_add_u32 m0, %[mv], 3072\n"
-    "s_movk_i32 %[so], 3072\n"
-    "s_nop 0\n"
-    "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
-    "s_waitcnt lgkmcnt(3)\n"
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r0], %[q0_8], %[c0]\n"
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r0], %[q1_8], %[c1]\n"
-    "ds_read_b128 %[r0], %[ka] offset:6144\n"
-    "s_add_u32 m0, %[mk], 4096\n"
-    "s_movk_i32 %[so], 4096\n"
-    "s_nop 0\n"
-    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n"
-    "s_waitcnt lgkmcnt(3)\n"
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r1], %[q0_9], %[c0]\n"
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r1], %[q1_9], %[c1]\n"
-    "ds_read_b128 %[r1], %[ka] offset:6656\n"
-    "s_add_u32 m0, %[mv], 4096\n"
-    "s_add_u32 %[so], %[sv], 0\n"
-    "s_nop 0\n"
-    "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
-    "s_waitcnt lgkmcnt(3)\n"
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r2], %[q0_10], %[c0]\n"
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r2], %[q1_10], %[c1]\n"
-    "ds_read_b128 %[r2], %[ka] offset:7168\n"
-    "s_add_u32 m0, %[mk], 5120\n"
-    "s_movk_i32 %[so], 5120\n"
-    "s_nop 0\n"
-    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n"
-    "s_waitcnt lgkmcnt(3)\n"
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r3], %[q0_11], %[c0]\n"
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r3], %[q1_11], %[c1]\n"
-    "ds_read_b128 %[r3], %[ka] offset:7680\n"
-    "s_add_u32 m0, %[mv], 5120\n"
-    "s_add_u32 %[so], %[sv], 1024\n"
-    "s_nop 0\n"
-    "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
-    "s_waitcnt lgkmcnt(3)\n"
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r0], %[q0_12], %[c0]\n"
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r0], %[q1_12], %[c1]\n"
-    "s_add_u32 m0, %[mk], 6144\n"
-    "s_movk_i32 %[so], 6144\n"
-    "s_nop 0\n"
-    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n"
-    "s_waitcnt lgkmcnt(2)\n"
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r1], %[q0_13], %[c0]\n"
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r1], %[q1_13], %[c1]\n"
-    "s_add_u32 m0, %[mv], 6144\n"
-    "s_add_u32 %[so], %[sv], 2048\n"
-    "s_nop 0\n"
-    "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
-    "s_waitcnt lgkmcnt(1)\n"
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r2], %[q0_14], %[c0]\n"
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r2], %[q1_14], %[c1]\n"
-    "s_add_u32 m0, %[mk], 7168\n"
-    "s_movk_i32 %[so], 7168\n"
-    "s_nop 0\n"
-    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n"
-    "s_waitcnt lgkmcnt(0)\n"
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r3], %[q0_15], %[c0]\n"
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r3], %[q1_15], %[c1]\n"
-    "s_add_u32 m0, %[mv], 7168\n"
-    "s_add_u32 %[so], %[sv], 3072\n"
-    "s_nop 0\n"
-    "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
-    "s_nop 15\n"
-        : [c0] "=&v"(c0), [c1] "=&v"(c1), [r0] "=&v"(r0), [r1] "=&v"(r1), [r2] "=&v"(r2),
-          [r3] "=&v"(r3), [so] "=&s"(so)
-        : [ka] "v"(ka), [mk] "s"(mk), [mv] "s"(mv), [rk] "s"(rk), [rv] "s"(rv),
-          [vk] "v"(vk_off), [vv] "v"(vv_off), [sv] "s"(sv_off),
-          [q0_0] "v"(qf[0][0]), [q0_1] "v"(qf[0][1]), [q0_2] "v"(qf[0][2]), [q0_3] "v"(qf[0][3]),
-          [q0_4] "v"(qf[0][4]), [q0_5] "v"(qf[0][5]), [q0_6] "v"(qf[0][6]), [q0_7] "v"(qf[0][7]),
-          [q0_8] "v"(qf[0][8]), [q0_9] "v"(qf[0][9]), [q0_10] "v"(qf[0][10]), [q0_11] "v"(qf[0][11]),
-          [q0_12] "v"(qf[0][12]), [q0_13] "v"(qf[0][13]), [q0_14] "v"(qf[0][14]), [q0_15] "v"(qf[0][15]),
-          [q1_0] "v"(qf[1][0]), [q1_1] "v"(qf[1][1]), [q1_2] "v"(qf[1][2]), [q1_3] "v"(qf[1][3]),
-          [q1_4] "v"(qf[1][4]), [q1_5] "v"(qf[1][5]), [q1_6] "v"(qf[1][6]), [q1_7] "v"(qf[1][7]),
-          [q1_8] "v"(qf[1][8]), [q1_9] "v"(qf[1][9]), [q1_10] "v"(qf[1][10]), [q1_11] "v"(qf[1][11]),
-          [q1_12] "v"(qf[1][12]), [q1_13] "v"(qf[1][13]), [q1_14] "v"(qf[1][14]), [q1_15] "v"(qf[1][15])
+        "s_mov_b32 m0, %[mv]\n"
+        "s_nop 0\n"
+        "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
+        :
+        : [mv] "s"(mv), [rv] "s"(v_tile_src(t)), [vv] "v"(vv_off), [so] "s"(so)
         : "m0", "memory");
   };
 #pragma clang diagnostic pop
+#undef PF_VCOPY
+#undef PF_NOCOPY
+#undef PF_QK_ASM
+#undef ASM_OPERANDS
   auto tile_max = [&](const f32x16& sc) {
     float mt = sc[0];
 #pragma unroll
@@ -886,7 +895,7 @@ attn_prefill64_kernel(PrefillArgs a) {
     __syncthreads();
     {
       f32x16 c0, c1;
-      qk(0, nt > 1 ? 1 : 0, c0, c1);
+      qk(0, nt > 1 ? 1 : 0, c0, c1, true);
       if (mi::prefill64_diag(pw, 0)) mask(0, c0, c1);
       if (!exact) {  // a column with no visible key keeps kNegBig (weights 0)
         m[0] = fmaxf(tile_max(c0), kNegBig);
@@ -909,7 +918,7 @@ attn_prefill64_kernel(PrefillArgs a) {
         const _Float16* vs = vbuf0 + ((t - 1) & 1) * V_TILE_HALVES + v_lds_off;
         constexpr int vRing = 4;
         f32x16 c0, c1;
-        qk(t, tk, c0, c1);
+        qk(t, tk, c0, c1, false);
         if (mi::prefill64_diag(pw, t)) mask(t, c0, c1);  // wave-uniform
         // PV(t-1), with tile t's weights computed between its MFMAs.
         f16x8 vf[vRing];
@@ -936,6 +945,7 @@ attn_prefill64_kernel(PrefillArgs a) {
           const int s = idx >> 3, i = idx & 7;
           if (idx < 16)
             acc[0][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[idx % vRing], pprev[0][s], acc[0][i], 0, 0, 0);
+          if (idx < 8) copy_v_piece(t, idx);
           float xa = 0.f, ya_next = 0.f;
           if (idx < 16) xa = __builtin_amdgcn_exp2f(ya);
           if (idx < 15) ya_next = fmaf(score(2 * idx + 2), c2, -m[(idx + 1) >> 3]);
@@ -993,8 +1003,7 @@ attn_prefill64_kernel(PrefillArgs a) {
     return !exact && ovf_word[0] != 0;
   };
   if (walk(false)) {
-    // Max pass: every tile's QK, masked, folded into m (the V copies of the
-    // asm block land and are not read).
+    // Max pass: every tile's QK, masked, folded into m (no V copies).
     __syncthreads();  // every wave has read the flag word
     m[0] = m[1] = kNegBig;
 #pragma unroll
@@ -1005,7 +1014,7 @@ attn_prefill64_kernel(PrefillArgs a) {
       const int tk = t + 1 < nt ? t + 1 : t;
       if (mi::prefill64_active(pw, t)) {
         f32x16 c0, c1;
-        qk(t, tk, c0, c1);
+        qk(t, tk, c0, c1, false);
         if (mi::prefill64_diag(pw, t)) mask(t, c0, c1);
         m[0] = fmaxf(m[0], tile_max(c0));
         m[1] = fmaxf(m[1], tile_max(c1));
