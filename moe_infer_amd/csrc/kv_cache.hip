@@ -129,22 +129,38 @@ kv_pack_kernel(const _Float16* __restrict__ k, const _Float16* __restrict__ v,
 // item count fits): the row / head / chunk of an item come from shifts and
 // one 32-bit division by G instead of the generic kernel's 64-bit divisions
 // by run-time values, which cost more than the copy's own instructions.
+// BLOCKED orders the K items by destination: item (32-row block, head, row
+// half u, chunk c, row slot j) with j fastest, so a wave stores 1 KiB of
+// contiguous block layout (four chunks of 16 row slots) and reads 64-byte
+// pieces of 16 rows; items whose row lies outside [pos, pos+n) do nothing.
+// Row-major order (each wave storing 16 bytes every 256) suits a few rows.
+template <bool BLOCKED>
 __global__ void __launch_bounds__(256)
 kv_pack256_kernel(const _Float16* __restrict__ k, const _Float16* __restrict__ v,
                   _Float16* __restrict__ kblk, _Float16* __restrict__ vblk, int64_t pos,
-                  uint32_t n, uint32_t G, uint32_t nblk) {
+                  uint32_t n, uint32_t G, uint32_t nblk, uint32_t nkblk) {
   constexpr int D = mi::kHeadDim;
   constexpr uint32_t cvec = D / 8;  // 16-byte chunks per head row
-  const uint32_t nk = n * G * cvec;
+  const uint32_t nk = BLOCKED ? nkblk * G * 2 * cvec * 16 : n * G * cvec;
   const uint32_t total = nk + nblk * G * cvec;
   const int64_t b_first = pos / MI_KV_VBLOCK;
   for (uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += gridDim.x * blockDim.x) {
     if (idx < nk) {
-      const uint32_t rh = idx / cvec, c = idx % cvec;
-      const uint32_t rr = rh / G, h = rh - rr * G;
-      *(f16x8*)(kblk + mi::k_offset(pos + rr, (int)h, 8 * c, (int)G, D)) =
-          *(const f16x8*)(k + ((int64_t)rr * G + h) * D + 8 * c);
+      if (BLOCKED) {
+        const uint32_t j = idx & 15, c = (idx >> 4) % cvec, u = (idx >> 4) / cvec & 1;
+        const uint32_t bh = idx / (32 * cvec), bb = bh / G, h = bh - bb * G;
+        const int64_t b = pos / MI_KV_KBLOCK + bb;
+        const int64_t r = b * MI_KV_KBLOCK + (((j >> 2) << 3) | (u << 2) | (j & 3));
+        if (r < pos || r >= pos + n) continue;
+        *(f16x8*)(kblk + ((((b * G + h) * 2 + u) * cvec + c) * 16 + j) * 8) =
+            *(const f16x8*)(k + ((r - pos) * G + h) * D + 8 * c);
+      } else {
+        const uint32_t rh = idx / cvec, c = idx % cvec;
+        const uint32_t rr = rh / G, h = rh - rr * G;
+        *(f16x8*)(kblk + mi::k_offset(pos + rr, (int)h, 8 * c, (int)G, D)) =
+            *(const f16x8*)(k + ((int64_t)rr * G + h) * D + 8 * c);
+      }
       continue;
     }
     const uint32_t vi = idx - nk;
@@ -313,9 +329,20 @@ mi_status kv_pack_rows(const _Float16* k, const _Float16* v, _Float16* dst_k, _F
   const int64_t nblk = (pos + n - 1) / MI_KV_VBLOCK - pos / MI_KV_VBLOCK + 1;
   const int64_t items = (n + nblk) * G * (D / 8);
   const int grid = (int)std::min<int64_t>((items + 255) / 256, 4096);
+  // destination-ordered K items from a few blocks' worth of rows on
+  const int64_t nkblk = (pos + n - 1) / MI_KV_KBLOCK - pos / MI_KV_KBLOCK + 1;
+  const int64_t bitems = (nkblk * MI_KV_KBLOCK + nblk) * G * (D / 8);
+  const bool blocked = n >= 4 * MI_KV_KBLOCK;
+  const int bgrid = (int)std::min<int64_t>((bitems + 255) / 256, 4096);
+  if (D == kHeadDim && blocked && bitems + (int64_t)bgrid * 256 < ((int64_t)1 << 32)) {
+    MI_HIP(mi::launch("kv_pack", kv_pack256_kernel<true>, dim3(bgrid), dim3(256), 0, stream, k, v,
+                      dst_k, dst_v, pos, (uint32_t)n, (uint32_t)G, (uint32_t)nblk,
+                      (uint32_t)nkblk));
+    return MI_OK;
+  }
   if (D == kHeadDim && items + (int64_t)grid * 256 < ((int64_t)1 << 32)) {
-    MI_HIP(mi::launch("kv_pack", kv_pack256_kernel, dim3(grid), dim3(256), 0, stream, k, v, dst_k,
-                      dst_v, pos, (uint32_t)n, (uint32_t)G, (uint32_t)nblk));
+    MI_HIP(mi::launch("kv_pack", kv_pack256_kernel<false>, dim3(grid), dim3(256), 0, stream, k, v,
+                      dst_k, dst_v, pos, (uint32_t)n, (uint32_t)G, (uint32_t)nblk, 0u));
     return MI_OK;
   }
   MI_HIP(mi::launch("kv_pack", kv_pack_kernel, dim3(grid), dim3(256), 0, stream, k, v, dst_k,

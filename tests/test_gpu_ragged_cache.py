@@ -178,6 +178,26 @@ def test_append_download_bit_exact_and_rollback():
     assert np.array_equal(kd.view(np.uint16), m.k[0][:pos].view(np.uint16))  # reset erases nothing
 
 
+@pytest.mark.parametrize("row0,n", [(37, 300), (64, 128), (5, 1000), (96, 130)])
+def test_long_unaligned_append_keeps_neighbours(row0, n):
+    """Appends of 128 rows or more take the destination-ordered K path:
+    rows before row0 and from row0 + n on keep their contents, bit for bit."""
+    announce(f"long append row0={row0} n={n}")
+    rng = np.random.default_rng(row0 * 7 + n)
+    c = Cache(num_layers=1, capacity=2048)
+    cap = c.capacity
+    base_k, base_v = f16(rng, cap, G * D), f16(rng, cap, G * D)
+    c.upload(0, base_k, base_v)
+    k, v = f16(rng, n, G * D), f16(rng, n, G * D)
+    c.set_pos(row0)
+    kv_cache_append(c, 0, dev(k), dev(v), row0)
+    ek, ev = base_k.copy(), base_v.copy()
+    ek[row0:row0 + n], ev[row0:row0 + n] = k, v
+    kd, vd = c.download(0, rows=cap)
+    assert np.array_equal(kd.view(np.uint16), ek.view(np.uint16))
+    assert np.array_equal(vd.view(np.uint16), ev.view(np.uint16))
+
+
 def test_upload_unaligned_rows_and_growth():
     rng = np.random.default_rng(13)
     c = Cache(num_layers=1, capacity=256)
