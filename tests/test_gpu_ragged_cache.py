@@ -178,10 +178,11 @@ def test_append_download_bit_exact_and_rollback():
     assert np.array_equal(kd.view(np.uint16), m.k[0][:pos].view(np.uint16))  # reset erases nothing
 
 
-@pytest.mark.parametrize("row0,n", [(37, 300), (64, 128), (5, 1000), (96, 130)])
+@pytest.mark.parametrize("row0,n", [(37, 300), (64, 128), (5, 1000), (96, 130), (3, 127), (31, 129)])
 def test_long_unaligned_append_keeps_neighbours(row0, n):
-    """Appends of 128 rows or more take the destination-ordered K path:
-    rows before row0 and from row0 + n on keep their contents, bit for bit."""
+    """Appends of 128 rows or more take the destination-ordered K path, fewer
+    the row-major one (n = 127): rows before row0 and from row0 + n on keep
+    their contents, and the appended rows land, bit for bit."""
     announce(f"long append row0={row0} n={n}")
     rng = np.random.default_rng(row0 * 7 + n)
     c = Cache(num_layers=1, capacity=2048)
