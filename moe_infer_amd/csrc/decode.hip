@@ -39,6 +39,10 @@ namespace {
 constexpr int D = mi::kHeadDim;
 constexpr float kNegBig = -1e30f;
 
+// Most sequences of a ragged batch whose tile offsets the flat split
+// computes itself (no plan launch); larger batches run ragged_plan_kernel.
+constexpr int kFusedPlan = 256;
+
 struct SplitArgs {
   const _Float16* k;        // K 32-row blocks (mi::k_offset)
   const _Float16* v;        // V blocks, (r,h,i) at v + ((r/8)*G + h)*D*8 + i*8 + r%8
@@ -58,6 +62,11 @@ struct SplitArgs {
   // concatenation and writes one partial per sequence it touches, in slot
   // x + s.  Null otherwise.
   const int32_t* tile_off;
+  // Flat split of up to kFusedPlan sequences: no plan kernel; every
+  // workgroup computes the tile offsets into LDS from lengths / offsets, and
+  // workgroup 0 also stores them here (= tile_off) for the merge kernel.
+  // Null otherwise.
+  int32_t* tile_off_out;
   int batch;
   // Optional fused append (decode step, verify): rows [app0, app0 + app_n)
   // of the cache are written from app_k / app_v ([app_n][G*D] token-major)
@@ -389,10 +398,55 @@ attn_split_kernel(SplitArgs a, X x) {
   constexpr bool flat = FLAT;  // the flat ragged split (a.tile_off)
   int64_t len = 0, row0 = 0, lim0 = 0, key_begin = 0, key_end = 0;
   int64_t t_lo = 0, t_hi = 0;  // flat: this workgroup's tiles of the concatenation
+  // flat: the tile offsets, from the plan kernel's table or computed below
+  int32_t* const ltoff = (int32_t*)(smem + GH * (NWH * ncols * (D + 4) + 2 * NWH * ncols));
+  auto toff = [&](int i) -> int64_t {  // tile_off[i], i wave-uniform in [0, batch]
+    return __builtin_amdgcn_readfirstlane(a.tile_off_out ? ltoff[i] : a.tile_off[i]);
+  };
   if constexpr (flat) {
+    if (a.tile_off_out) {  // uniform
+      // Wave 0 scans the tile counts (an invalid descriptor counts 0) of up
+      // to kFusedPlan sequences, 64 per step, into LDS; workgroup (0, 0)
+      // also stores them for the merge kernel.
+      if (wv == 0) {
+        int32_t n[kFusedPlan / 64];
+#pragma unroll
+        for (int c = 0; c < kFusedPlan / 64; c++) {
+          const int i = 64 * c + lane;
+          n[c] = 0;
+          if (i < a.batch) {
+            const int32_t len = a.lengths[i], off = a.offsets[i];
+            const bool bad = len < 0 || len > a.kv_len || off < 0 || (off & 31);
+            n[c] = bad ? 0 : (len + 31) >> 5;
+          }
+        }
+        const bool store = blockIdx.x == 0 && blockIdx.y == 0;
+        int32_t carry = 0;
+#pragma unroll
+        for (int c = 0; c < kFusedPlan / 64; c++) {
+          int32_t inc = n[c];
+#pragma unroll
+          for (int d = 1; d < 64; d <<= 1) {
+            const int32_t y = __shfl_up(inc, d, 64);
+            if (lane >= d) inc += y;
+          }
+          const int i = 64 * c + lane;
+          if (i < a.batch) {
+            ltoff[i] = carry + inc - n[c];
+            if (store) a.tile_off_out[i] = carry + inc - n[c];
+          }
+          carry += __shfl(inc, 63, 64);
+        }
+        if (lane == 0) {
+          ltoff[a.batch] = carry;
+          if (store) a.tile_off_out[a.batch] = carry;
+        }
+      }
+      __syncthreads();
+    }
     // min(gridDim.x, T) workgroups take the tiles, each at least one
     // (uniform values: kept in scalar registers)
-    const int64_t total = __builtin_amdgcn_readfirstlane(a.tile_off[a.batch]);
+    const int64_t total = toff(a.batch);
     const int64_t nw = min((int64_t)gridDim.x, total);
     if (chunk_idx >= nw) return;  // uniform
     t_lo = (int64_t)chunk_idx * total / nw;
@@ -401,7 +455,7 @@ attn_split_kernel(SplitArgs a, X x) {
     int lo = 0, hi = a.batch - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if (__builtin_amdgcn_readfirstlane(a.tile_off[mid]) <= t_lo) lo = mid;
+      if (toff(mid) <= t_lo) lo = mid;
       else hi = mid - 1;
     }
     s = lo;
@@ -529,8 +583,8 @@ attn_split_kernel(SplitArgs a, X x) {
   for (;;) {
   int64_t pslot = (int64_t)s * a.max_chunks + chunk_idx;  // partial slot
   if constexpr (flat) {
-    const int64_t ps = __builtin_amdgcn_readfirstlane(a.tile_off[s]);
-    const int64_t pe = __builtin_amdgcn_readfirstlane(a.tile_off[s + 1]);
+    const int64_t ps = toff(s);
+    const int64_t pe = toff(s + 1);
     len = __builtin_amdgcn_readfirstlane(a.lengths[s]);
     row0 = __builtin_amdgcn_readfirstlane(a.offsets[s]);
     lim0 = len;
@@ -742,11 +796,10 @@ attn_split_kernel(SplitArgs a, X x) {
     }
     break;
   }
-  if (__builtin_amdgcn_readfirstlane(a.tile_off[s + 1]) >= t_hi) break;
+  if (toff(s + 1) >= t_hi) break;
   // next sequence with tiles (the range ends inside a later one)
   do s++;
-  while (__builtin_amdgcn_readfirstlane(a.tile_off[s + 1]) ==
-         __builtin_amdgcn_readfirstlane(a.tile_off[s]));
+  while (toff(s + 1) == toff(s));
   __syncthreads();  // the LDS merge area is reused
   }
 }
@@ -995,6 +1048,7 @@ mi_status launch_split(const SplitArgs& a, int64_t batch, hipStream_t stream, co
   const int ncols = a.nq * 8;
   size_t lds = (size_t)GH * (NWH * ncols * (D + 4) + 2 * NWH * ncols) * sizeof(float);
   if constexpr (is_proj<X>::value) lds += (size_t)GH * 8 * (D + 8) * sizeof(_Float16);
+  if constexpr (FLAT) lds += (size_t)(kFusedPlan + 1) * sizeof(int32_t);
   static std::atomic<uint64_t> lds_set{0};
   // (below 160 KiB: the kernel also holds a few bytes of static LDS)
   MI_TRY(mi::set_lds_limit((const void*)attn_split_kernel<NWH, NCB, GH, X, FLAT>, 159 * 1024, lds_set));
@@ -1087,6 +1141,7 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
   a.app0 = app.row0;
   a.app_n = app.n;
   a.tile_off = nullptr;
+  a.tile_off_out = nullptr;
   a.batch = (int)batch;
   const int nwg = ragged_nwg(G, plan.gh);
   const size_t need = lengths ? ragged_workspace_bytes(batch, G, nwg)
@@ -1103,8 +1158,12 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
     if ((int64_t)batch * ((max_len + 31) / 32) >= ((int64_t)1 << 31))
       return mi::fail(MI_ERR_UNSUPPORTED, "batch * max_len / 32 beyond 2^31 tiles");
     int32_t* tile_off = (int32_t*)(a.part_ml + slots * G * nq * 8 * 2);
-    MI_HIP(mi::launch("ragged_plan", ragged_plan_kernel, dim3(1), dim3(256), 0, stream, lengths,
-                      offsets, (int)batch, kv_len, tile_off));
+    if (batch <= kFusedPlan) {
+      a.tile_off_out = tile_off;  // the split launch computes and stores them
+    } else {
+      MI_HIP(mi::launch("ragged_plan", ragged_plan_kernel, dim3(1), dim3(256), 0, stream, lengths,
+                        offsets, (int)batch, kv_len, tile_off));
+    }
     a.tile_off = tile_off;
     a.max_chunks = nwg;
     a.chunk = 0;
@@ -1396,8 +1455,9 @@ extern "C" mi_status mi_attn_step_proj(mi_kv* kv, int32_t layer, const float* q_
 // the library runs on holds its own copy until the process ends; host code
 // reaches it only through the address hipGetSymbolAddress returns for the
 // current device (the array's name in host code is not a device address).
-// Nothing in it has to start at zero: the plan kernel writes every tile
-// offset and the split kernel writes every partial slot the merge reads.
+// Nothing in it has to start at zero: the plan kernel (or, for up to
+// kFusedPlan sequences, the split launch itself) writes every tile offset
+// and the split kernel writes every partial slot the merge reads.
 static __device__ __align__(256) unsigned char scratch[MI_NOALLOC_SCRATCH_BYTES];
 
 namespace {
