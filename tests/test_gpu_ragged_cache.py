@@ -82,13 +82,15 @@ def test_ragged_rejects_bad_tables():
                                torch.tensor(ln, dtype=torch.int32).cuda(), q, 64)
 
 
-def test_ragged_many_sequences_flat_split():
-    """600 sequences (the tile-offset scan runs over three 256-sequence
-    blocks), lengths 0..300 with exact multiples of 32 among them: every
-    output equals the oracle, zero-length sequences are zero."""
-    announce("ragged 600 seqs")
-    rng = np.random.default_rng(600)
-    lengths = rng.integers(0, 301, size=600).astype(np.int32)
+@pytest.mark.parametrize("b", [600, 256, 200])
+def test_ragged_many_sequences_flat_split(b):
+    """Many sequences, lengths 0..300 with exact multiples of 32 among them:
+    every output equals the oracle, zero-length sequences are zero.  600 runs
+    the plan kernel's scan over three 256-sequence blocks; 256 and 200 the
+    split launch's own scan (full and partial last 64-lane step)."""
+    announce(f"ragged {b} seqs")
+    rng = np.random.default_rng(b)
+    lengths = rng.integers(0, 301, size=b).astype(np.int32)
     lengths[::7] = 0
     lengths[3::11] = 64
     lengths[5::13] = 32
@@ -100,7 +102,7 @@ def test_ragged_many_sequences_flat_split():
                              torch.from_numpy(lengths).cuda(), dev(q), int(lengths.max()),
                              gate=dev(g))
     ref = O.decode_ragged(q, k, v, offsets, lengths, gate=g)
-    assert_close(out, ref, "ragged 600 seqs")
+    assert_close(out, ref, f"ragged {b} seqs")
     assert np.all(host(out)[lengths == 0] == 0)
 
 
