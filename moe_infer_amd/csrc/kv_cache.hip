@@ -130,9 +130,10 @@ kv_pack_kernel(const _Float16* __restrict__ k, const _Float16* __restrict__ v,
 // one 32-bit division by G instead of the generic kernel's 64-bit divisions
 // by run-time values, which cost more than the copy's own instructions.
 // BLOCKED orders the K items by destination: item (32-row block, head, row
-// half u, chunk c, row slot j) with j fastest, so a wave stores 1 KiB of
-// contiguous block layout (four chunks of 16 row slots) and reads 64-byte
-// pieces of 16 rows; items whose row lies outside [pos, pos+n) do nothing.
+// half u, chunk c, row slot j) with j fastest, so each store instruction of
+// a wave writes 1 KiB of contiguous block layout (four chunks of 16 row
+// slots) and each load reads 64-byte pieces of 16 rows; items whose row lies
+// outside [pos, pos+n) do nothing.
 // Row-major order (each wave storing 16 bytes every 256) suits a few rows.
 template <bool BLOCKED>
 __global__ void __launch_bounds__(256)
@@ -141,20 +142,29 @@ kv_pack256_kernel(const _Float16* __restrict__ k, const _Float16* __restrict__ v
                   uint32_t n, uint32_t G, uint32_t nblk, uint32_t nkblk) {
   constexpr int D = mi::kHeadDim;
   constexpr uint32_t cvec = D / 8;  // 16-byte chunks per head row
-  const uint32_t nk = BLOCKED ? nkblk * G * 2 * cvec * 16 : n * G * cvec;
+  // BLOCKED: one item moves four chunks c0 + 4 i of one row slot (loads
+  // first, 64 bytes of the source row; then four stores)
+  const uint32_t nk = BLOCKED ? nkblk * G * 2 * cvec * 4 : n * G * cvec;
   const uint32_t total = nk + nblk * G * cvec;
   const int64_t b_first = pos / MI_KV_VBLOCK;
   for (uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += gridDim.x * blockDim.x) {
     if (idx < nk) {
       if (BLOCKED) {
-        const uint32_t j = idx & 15, c = (idx >> 4) % cvec, u = (idx >> 4) / cvec & 1;
-        const uint32_t bh = idx / (32 * cvec), bb = bh / G, h = bh - bb * G;
+        // idx = (((bh * 2 + u) * 2 + cq) * 4 + cg) * 16 + j, c0 = 16 cq + cg
+        const uint32_t j = idx & 15, c0 = 16 * ((idx >> 6) & 1) + ((idx >> 4) & 3);
+        const uint32_t u = (idx >> 7) & 1;
+        const uint32_t bh = idx >> 8, bb = bh / G, h = bh - bb * G;
         const int64_t b = pos / MI_KV_KBLOCK + bb;
         const int64_t r = b * MI_KV_KBLOCK + (((j >> 2) << 3) | (u << 2) | (j & 3));
         if (r < pos || r >= pos + n) continue;
-        *(f16x8*)(kblk + ((((b * G + h) * 2 + u) * cvec + c) * 16 + j) * 8) =
-            *(const f16x8*)(k + ((r - pos) * G + h) * D + 8 * c);
+        const _Float16* src = k + ((r - pos) * G + h) * D + 8 * c0;
+        _Float16* dst = kblk + ((((b * G + h) * 2 + u) * cvec + c0) * 16 + j) * 8;
+        f16x8 x[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) x[i] = *(const f16x8*)(src + 32 * i);
+#pragma unroll
+        for (int i = 0; i < 4; i++) *(f16x8*)(dst + 4 * 16 * 8 * i) = x[i];
       } else {
         const uint32_t rh = idx / cvec, c = idx % cvec;
         const uint32_t rr = rh / G, h = rh - rr * G;
@@ -331,7 +341,7 @@ mi_status kv_pack_rows(const _Float16* k, const _Float16* v, _Float16* dst_k, _F
   const int grid = (int)std::min<int64_t>((items + 255) / 256, 4096);
   // destination-ordered K items from a few blocks' worth of rows on
   const int64_t nkblk = (pos + n - 1) / MI_KV_KBLOCK - pos / MI_KV_KBLOCK + 1;
-  const int64_t bitems = (nkblk * MI_KV_KBLOCK + nblk) * G * (D / 8);
+  const int64_t bitems = (nkblk * MI_KV_KBLOCK / 4 + nblk) * G * (D / 8);
   const bool blocked = n >= 4 * MI_KV_KBLOCK;
   const int bgrid = (int)std::min<int64_t>((bitems + 255) / 256, 4096);
   if (D == kHeadDim && blocked && bitems + (int64_t)bgrid * 256 < ((int64_t)1 << 32)) {
