@@ -180,6 +180,33 @@ ORACLE_API void oracle_sigmoid_gate_inplace(float* out, const float* gate,
   }
 }
 
+/* One decode step of the reference's f32 attention core (the four functions
+ * above, in the order cpu.rs:149-163 calls them), with the query heads
+ * spread over `threads` OpenMP threads.  Each head runs the same scalar
+ * loops as the batched functions (called with one head and the head's K / V
+ * column offset), so the result equals the single-threaded one bit for bit.
+ * A CPU baseline variant only; the reference runs its attention on one
+ * thread. */
+ORACLE_API void oracle_decode_heads_omp(const float* q, const float* k_cache,
+                                        const float* v_cache, const float* gate,
+                                        float* scores, float* out, int64_t num_q_heads,
+                                        int64_t num_kv_heads, int64_t head_dim,
+                                        int64_t kv_dim, int64_t seq_len, int64_t max_seq,
+                                        int threads) {
+  const int64_t n_rep = num_q_heads / num_kv_heads;
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t qh = 0; qh < num_q_heads; qh++) {
+    const int64_t kh = qh / n_rep;
+    float* s = scores + qh * max_seq;
+    oracle_attention_scores_batched(q + qh * head_dim, k_cache + kh * head_dim, s, 1, 1,
+                                    head_dim, kv_dim, seq_len, max_seq);
+    oracle_attention_softmax_batched(s, 1, seq_len, max_seq);
+    oracle_attention_values_batched(s, v_cache + kh * head_dim, out + qh * head_dim, 1, 1,
+                                    head_dim, kv_dim, seq_len, max_seq);
+    if (gate) oracle_sigmoid_gate_inplace(out + qh * head_dim, gate + qh * head_dim, head_dim);
+  }
+}
+
 /* src/engine/qwen35_moe/mtp.rs:304-350  cpu_attention (MTP layer form:
  * normalisation by sum_exp inside the P.V loop, no sum > 0 guard). */
 ORACLE_API void oracle_mtp_cpu_attention(const float* q, const float* k_cache,

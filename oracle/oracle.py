@@ -45,6 +45,8 @@ def lib() -> C.CDLL:
             "oracle_attention_values_batched": (None, [P, P, P, I64, I64, I64, I64, I64, I64]),
             "oracle_kv_cache_append": (None, [P, P, P, P, I64, I64]),
             "oracle_sigmoid_gate_inplace": (None, [P, P, I64]),
+            "oracle_decode_heads_omp": (None, [P, P, P, P, P, P, I64, I64, I64, I64, I64, I64,
+                                               C.c_int]),
             "oracle_mtp_cpu_attention": (None, [P, P, P, P, I64, I64, I64, I64, C.c_float]),
             "oracle_attn_decode_f32": (None, [P, P, P, P, I64, I64, I64, I64, P]),
             "oracle_attn_decode_f16": (None, [P, P, P, P, I64, I64, I64, I64, P]),
@@ -337,4 +339,13 @@ class DecodeBaseline:
         L.oracle_attention_softmax_batched(scores, H, seq_len, self.max_seq)
         L.oracle_attention_values_batched(scores, v, out, H, G, D, G * D, seq_len, self.max_seq)
         L.oracle_sigmoid_gate_inplace(out, gate, H * D)
+        return self.out.reshape(H, D)
+
+    def run_omp(self, seq_len: int, threads: int) -> np.ndarray:
+        """The same step with the query heads spread over `threads` OpenMP
+        threads (same per-head loops, same bits)."""
+        q, gate, k, v, scores, out = self._args
+        H, G, D = self.H, self.G, self.D
+        lib().oracle_decode_heads_omp(q, k, v, gate, scores, out, H, G, D, G * D, seq_len,
+                                      self.max_seq, threads)
         return self.out.reshape(H, D)

@@ -222,3 +222,19 @@ def test_cache_model_semantics():
     assert m.k[0].shape[0] == 8 and m.len[0] == 6 and np.all(m.k[0][0] == 1)
     m.reset()
     assert m.pos == 0 and m.len == [0, 0] and np.all(m.k[0][1] == 5)
+
+
+@pytest.mark.parametrize("threads", [1, 3, 16])
+def test_decode_baseline_heads_over_threads_same_bits(rng, threads):
+    """The CPU baseline's OpenMP variant (query heads over threads) runs the
+    same per-head loops: bit-equal to the single-threaded step, and close to
+    the f64 decode."""
+    H, G, D, L = 16, 2, 256, 300
+    q, g = f16(rng, H * D), f16(rng, H * D)
+    k, v = f16(rng, 512, G * D), f16(rng, 512, G * D)
+    base = O.DecodeBaseline(q, k, v, g)
+    one = base.run(L).copy()
+    many = base.run_omp(L, threads).copy()
+    assert np.array_equal(one.view(np.uint32), many.view(np.uint32))
+    ref = O.decode_f64(q, k[:L], v[:L], L, gate=g)
+    assert np.max(np.abs(one - ref.reshape(H, D))) < 1e-5
