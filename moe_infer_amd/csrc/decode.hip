@@ -64,7 +64,7 @@ struct SplitArgs {
   const int32_t* tile_off;
   // Flat split of up to kFusedPlan sequences: no plan kernel; every
   // workgroup computes the tile offsets into LDS from lengths / offsets, and
-  // workgroup 0 also stores them here (= tile_off) for the merge kernel.
+  // workgroup (0, 0) also stores them here (= tile_off) for the merge kernel.
   // Null otherwise.
   int32_t* tile_off_out;
   int batch;
