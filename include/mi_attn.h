@@ -202,8 +202,9 @@ mi_status mi_attn_verify(mi_kv* kv, int32_t layer, const mi_f16* q,
  * blocks).  offsets, lengths: device int32[batch].  q, gate, out:
  * [batch][H][D].  max_len >= every lengths[s]; batch <= 65535 (else
  * MI_ERR_UNSUPPORTED).  The sequences' 32-row tiles are split evenly over the
- * CUs (one launch computes the tile offsets on the device, one attends, one
- * merges), so a batch of unequal lengths keeps every CU busy.
+ * CUs (one launch attends, one merges; the attending launch computes the
+ * tile offsets itself for up to 256 sequences, a launch before it does for
+ * larger batches), so a batch of unequal lengths keeps every CU busy.
  * No reference counterpart (the reference decodes one sequence,
  * README.md:150-165); per-sequence math is mi_attn_decode's.  Needs a
  * device workspace of mi_attn_ragged_workspace_size bytes. */
