@@ -326,7 +326,7 @@ def main():
     # ---------------------------------------------------------------- C5 verify
     if not only or "verify" in only:
         nl = 4  # 4 x 128 MiB of K/V: more than the last-level cache
-        cache = mi.Cache(num_layers=nl, capacity=C5_CTX + C5_K)
+        cache = mi.Cache(num_layers=nl, capacity=C5_CTX + 16)
         for layer in range(nl):
             mi.kv_cache_append(cache, layer, randn(C5_CTX, G * D, seed=600 + layer),
                                randn(C5_CTX, G * D, seed=700 + layer), 0)
@@ -348,6 +348,31 @@ def main():
         rec["verify"] = {"us_per_layer": us_call, "gbps": C5_BYTES / (us_call * 1e3),
                          "split_kernel_us": split_us, "bytes": C5_BYTES}
         print(f"[bench] verify {us_call:.2f} us/layer", file=sys.stderr, flush=True)
+        # The same call with 16 draft tokens: the wide verify (one split pass
+        # reading each K/V tile once for all 16 tokens), and for comparison
+        # the same tokens as four 4-token groups (MI_ATTN_VERIFY_WIDE=0).
+        q16, k16 = randn(16, H, D, seed=55), randn(16, G * D, seed=56)
+        v16, g16 = randn(16, G * D, seed=57), randn(16, H, D, seed=58)
+        out16 = torch.empty_like(q16)
+
+        def verify16():
+            for layer in range(nl):
+                mi.attn_verify(cache, layer, q16, k16, v16, C5_CTX, gate=g16, out=out16)
+            cache.set_pos(C5_CTX + 2)
+
+        ms16 = timed(verify16, args.steps, args.warmup, backlog_ms=args.steps * nl * 0.4 + 20)
+        _lib.prof_enable(False)
+        os.environ["MI_ATTN_VERIFY_WIDE"] = "0"
+        try:
+            ms16g = timed(verify16, args.steps, args.warmup,
+                          backlog_ms=args.steps * nl * 1.2 + 20)
+        finally:
+            del os.environ["MI_ATTN_VERIFY_WIDE"]
+        _lib.prof_enable(False)
+        rec["verify"]["k16_us_per_layer"] = ms16 * 1000 / nl
+        rec["verify"]["k16_grouped_us_per_layer"] = ms16g * 1000 / nl
+        print(f"[bench] verify K=16 {ms16 * 1000 / nl:.2f} us/layer (as 4-token groups "
+              f"{ms16g * 1000 / nl:.2f})", file=sys.stderr, flush=True)
         del cache
 
     # ---------------------------------------------------------------- C3 ragged

@@ -187,9 +187,11 @@ mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
 
 /* K-token verify for speculative decoding: same contract as mi_attn_prefill
  * (append at past_pos, query i attends [0, past_pos + i]) for small n, run
- * as a split-K HBM-bound kernel over the cache instead of the MFMA prefill
- * tiles.  Rollback afterwards is mi_kv_set_pos.  k = v = NULL as for
- * mi_attn_prefill. */
+ * split-K over the cache: up to 4 tokens in the decode kernel's form, 5..16
+ * tokens in one pass of the prefill's MFMA tiles over key chunks that reads
+ * each K/V tile once for all tokens (MI_ATTN_VERIFY_WIDE=0 runs them as
+ * 4-token groups instead), then a merge.  Rollback afterwards is
+ * mi_kv_set_pos.  k = v = NULL as for mi_attn_prefill. */
 mi_status mi_attn_verify(mi_kv* kv, int32_t layer, const mi_f16* q,
                          const mi_f16* k, const mi_f16* v, const mi_f16* gate,
                          mi_f16* out, int64_t past_pos, int32_t n,

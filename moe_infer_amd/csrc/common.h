@@ -191,6 +191,14 @@ size_t merge_state_bytes(int G);
 // Whether workgroup b of a launch runs on XCD b % 8 on the current device,
 // checked once per device with a probe kernel (decode.hip).
 bool xcd_round_robin();
+// The wide verify's split pass (prefill.hip): attn_prefill64_kernel in its
+// verify form over `nchunks` chunks of `chunk` keys (a multiple of 64) of
+// rows [0, past + n) of `layer`, n <= 16 query tokens q [n][H][D]; writes
+// the unnormalised partials part_o [G][nchunks][8 n][D] and part_ml
+// [G][nchunks][8 n][2] that attn_combine_kernel merges.
+mi_status verify_wide_split(const mi_kv* kv, int32_t layer, const _Float16* q, int64_t past,
+                            int32_t n, int64_t chunk, int32_t nchunks, float* part_o,
+                            float* part_ml, hipStream_t stream);
 // Enqueues the row copy of kv_cache_append_n on `stream` (no len update).
 mi_status kv_append_rows(mi_kv* kv, int32_t layer, const _Float16* k,
                          const _Float16* v, int64_t pos, int32_t n,

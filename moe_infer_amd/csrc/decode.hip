@@ -1242,9 +1242,58 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
 // With k_new / v_new, the n new rows [past_pos, past_pos + n) are appended
 // by the split kernels themselves (each token group appends its own rows,
 // which precede every read of them); the caller has grown the cache.
+// Wide verify for 5..16 query tokens (MI_ATTN_VERIFY_WIDE=0, read at each
+// call, turns it off): one split pass that reads every K/V tile once for all
+// tokens (attn_prefill64_kernel's MFMA tiles over key chunks), then the
+// combine, instead of one split-K launch pair per 4-token group.
+bool verify_wide_enabled() {
+  const char* e = getenv("MI_ATTN_VERIFY_WIDE");
+  return !(e && *e && atoi(e) == 0);
+}
+
+mi_status wide_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float16* gate,
+                      _Float16* out, int64_t past_pos, int32_t n, hipStream_t stream,
+                      const _Float16* k_new, const _Float16* v_new) {
+  const int G = kv->G;
+  const int64_t rows = past_pos + n;
+  // about 256 workgroups of (chunk, KV head); whole 64-key tiles; at most
+  // kMaxChunks chunks (the combine's limit)
+  int64_t chunk = (rows * G + 255) / 256;
+  chunk = std::max<int64_t>(chunk, (rows + kMaxChunks - 1) / kMaxChunks);
+  chunk = (chunk + 63) / 64 * 64;
+  const int nchunks = (int)((rows + chunk - 1) / chunk);
+  const int ncols = 8 * n;
+  const size_t units = (size_t)G * nchunks * ncols;
+  void* ws;
+  MI_TRY(mi::kv_workspace(kv, units * (D + 2) * sizeof(float) + 256, stream, &ws));
+  float* part_o = (float*)ws;
+  float* part_ml = part_o + units * D;
+  if (k_new) MI_TRY(mi::kv_append_rows(kv, layer, k_new, v_new, past_pos, n, stream));
+  MI_TRY(mi::verify_wide_split(kv, layer, q, past_pos, n, chunk, nchunks, part_o, part_ml,
+                               stream));
+  CombineArgs c{};
+  c.kv_len = rows;
+  c.part_o = part_o;
+  c.part_ml = part_ml;
+  c.gate = gate;
+  c.out = out;
+  c.G = G;
+  c.H = kv->H;
+  c.nq = n;
+  c.chunk = (int)chunk;
+  c.max_chunks = nchunks;
+  c.batch = 1;
+  c.nslots = nchunks;
+  MI_HIP(mi::launch("attn_combine", attn_combine_kernel<32>, dim3(n * 8, G * (D / 32), 1),
+                    dim3(256), 0, stream, c));
+  return MI_OK;
+}
+
 mi_status cache_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float16* gate,
                        _Float16* out, int64_t past_pos, int32_t n, hipStream_t stream,
                        const _Float16* k_new = nullptr, const _Float16* v_new = nullptr) {
+  if (n > 4 && n <= 16 && verify_wide_enabled())
+    return wide_attend(kv, layer, q, gate, out, past_pos, n, stream, k_new, v_new);
   const int64_t lim0 = past_pos + 1;
   // The workspace is grown once, to the largest group's need, before any
   // launch: a growth refused under graph capture then leaves nothing of

@@ -79,6 +79,21 @@ MI_HD inline PrefillWave64 prefill_wave64(int past, int n, int qtile, int qb, in
   p.koff = 32 * kp;
   return p;
 }
+// The wide verify's form of the same: the workgroup's keys are chunk
+// [kbeg, kbeg + chunk) of [0, past + n), positions relative to kbeg; rows
+// 64 qb .. + 63 are tokens 8 qb .. 8 qb + 7 (each with the group's eight
+// heads), token i seeing keys up to past + i.
+MI_HD inline PrefillWave64 verify_wave64(int64_t past, int n, int64_t kbeg, int64_t chunk,
+                                         int qb, int kp) {
+  PrefillWave64 p;
+  p.first = (int)(past - kbeg) + 8 * qb;
+  p.last = p.first + 7;
+  const int64_t end = past + n - kbeg;
+  p.kv_len = (int)(end < chunk ? end : chunk);
+  p.nt = (p.kv_len + kPrefillBK - 1) / kPrefillBK;
+  p.koff = 32 * kp;
+  return p;
+}
 MI_HD inline bool prefill64_active(const PrefillWave64& p, int t) {
   return t * kPrefillBK + p.koff <= p.last;
 }

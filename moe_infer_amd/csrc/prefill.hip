@@ -62,6 +62,19 @@ struct PrefillArgs {
   float scale_log2e;
 };
 
+// Wide verify (attn_verify_wide_kernel): workgroup = (key chunk, KV head);
+// rows are (token, query head of the group) pairs, row = 8 token + head;
+// keys [c chunk, (c + 1) chunk) of [0, past + n); unnormalised partials
+// (O, m, l) go to part_o [G][nslots][ncols][D] / part_ml [..][2] for the
+// combine kernel (ncols = 8 n).
+struct VerifyArgs {
+  int64_t chunk;
+  int nchunks, ncols;
+  int64_t nslots;
+  float* part_o;
+  float* part_ml;
+};
+
 // Row m of a 32-key QK tile holds key swap_bits_2_3(m): then accumulator
 // element e of lane half hl (row 8*(e/4) + 4*hl + e%4) is key
 // 16*(e/8) + 8*hl + e%8, i.e. the PV step e/8 sees eight consecutive keys
@@ -531,626 +544,39 @@ attn_prefill_kernel(PrefillArgs a) {
 // The two key halves of a query row merge through LDS at the end: wave
 // (qb, kp) finishes column block kp of its rows.
 
-__global__ void __launch_bounds__(256, 1)
-attn_prefill64_kernel(PrefillArgs a) {
-  extern __shared__ _Float16 lds[];
-  const int lane = threadIdx.x & 63;
-  // (threadIdx.x >> 6 is wave-uniform, but a readfirstlane here, making the
-  // per-tile branches scalar, leads the register allocator to ~1300 spills)
-  const int w = threadIdx.x >> 6;
-  const int qb = w & 1;   // query half of the workgroup's 128 rows
-  const int kp = w >> 1;  // key half of each 64-key tile
-  const int hl = lane >> 5;
-  const int col = lane & 31;
+__global__ void __launch_bounds__(256, 1) attn_prefill64_kernel(PrefillArgs a) {
+  constexpr bool VERIFY = false;
+  const VerifyArgs vx{};
+#include "prefill64_body.inc"
+}
 
-  int kvh, hg, qtile;
-  if (!prefill_item(blockIdx.x, a, kvh, hg, qtile)) return;
-  const int hq = kvh * 8 + hg;
-  const int q0 = qtile * BQ;
+// The verify kernel takes the body through an inlined device template: the
+// body placed directly in the kernel spills 173 registers there.
+template <bool VERIFY>
+__device__ __forceinline__ void verify_wide_body(const PrefillArgs& a, const VerifyArgs& vx) {
+#include "prefill64_body.inc"
+}
 
-  // Q^T operands of the two column blocks: query q0 + 64 qb + 32 b + col.
-  f16x8 qf[2][16];
-#pragma unroll
-  for (int b = 0; b < 2; b++) {
-    const int qi = q0 + 64 * qb + 32 * b + col;
-    if (qi < a.n) {
-      const _Float16* qp = a.q + ((int64_t)qi * a.H + hq) * D + 8 * hl;
-#pragma unroll
-      for (int ks = 0; ks < 16; ks++) qf[b][ks] = *(const f16x8*)(qp + 16 * ks);
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < 16; ks++) qf[b][ks] = f16x8{};
-    }
-  }
-  const int past = (int)a.past;
-  const mi::PrefillWave64 pw = mi::prefill_wave64(past, a.n, qtile, qb, kp);
-  const int kv_len = pw.kv_len;
-  const int nt = pw.nt;
-  const float c2 = a.scale_log2e;
-  const int qpos0 = past + q0 + 64 * qb + col;  // block b: qpos0 + 32 b
+__global__ void __launch_bounds__(256, 1) attn_verify_wide_kernel(PrefillArgs a, VerifyArgs vx) {
+  verify_wide_body<true>(a, vx);
+}
 
-  f32x16 acc[2][8];
-#pragma unroll
-  for (int b = 0; b < 2; b++)
-#pragma unroll
-    for (int i = 0; i < 8; i++) acc[b][i] = f32x16{};
-  float m[2] = {kNegBig, kNegBig}, l[2] = {0.f, 0.f};
-
-  // Copies: the same pieces as attn_prefill_kernel (wave w moves K pieces
-  // 8w .. 8w+7: block w / 2, row half w % 2, column chunks 0..7; and V
-  // pieces 8w .. 8w+7: 8-key blocks 2w, 2w + 1, four 1-KiB pieces each).
-  const int lane16 = lane * 8;
-  const int wu = __builtin_amdgcn_readfirstlane(w);
-  const _Float16* kg = a.k + (int64_t)kvh * (32 * D);
-  const _Float16* vg = a.v + (int64_t)kvh * (D * 8);
-  const int64_t kblk_stride = (int64_t)a.G * (32 * D);
-  const int64_t vblk_stride = (int64_t)a.G * (D * 8);
-  _Float16* const kbuf0 = lds;
-  _Float16* const vbuf0 = lds + 2 * K_TILE_HALVES;
-  const int kb_w = wu >> 1, ku_w = wu & 1;
-  // byte offsets of this lane within a source tile (piece 0 of the wave)
-  const int vk_off = 2 * (lane16 + kb_w * (int)kblk_stride + ku_w * 8 * 512);
-  const int vv_off = 2 * (lane16 + 2 * wu * (int)vblk_stride);
-  const int sv_off = 2 * (int)vblk_stride;
-  auto lds_addr = [](const _Float16* p) {
-    return (int)(uintptr_t)(const __attribute__((address_space(3))) _Float16*)p;
-  };
-  auto k_tile_src = [&](int t) { return buf_rsrc(kg + (int64_t)(t * 2) * kblk_stride); };
-  auto v_tile_src = [&](int t) { return buf_rsrc(vg + (int64_t)(t * 8) * vblk_stride); };
-  auto k_piece_lds = [&](int t) {  // wave's K piece 0 of tile t
-    return lds_addr(kbuf0 + (t & 1) * K_TILE_HALVES + kb_w * KSUB + ku_w * KU);
-  };
-  auto v_piece_lds = [&](int t) {
-    return lds_addr(vbuf0 + (t & 1) * V_TILE_HALVES + 8 * wu * 512);
-  };
-  auto load_k_piece = [&](int t, int pi) {
-    _Float16* ks = kbuf0 + (t & 1) * K_TILE_HALVES;
-    const int i = 8 * wu + pi;
-    const int b = i >> 4, u = (i >> 3) & 1, pc = i & 7;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        k_tile_src(t), (__attribute__((address_space(3))) void*)(ks + b * KSUB + u * KU + pc * 512), 16,
-        2 * (lane16 + b * (int)kblk_stride + (u * 8 + pc) * 512), 0, 0, 0);
-  };
-  auto load_v_piece = [&](int t, int pi) {
-    _Float16* vs = vbuf0 + (t & 1) * V_TILE_HALVES;
-    const int i = 8 * wu + pi;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        v_tile_src(t), (__attribute__((address_space(3))) void*)(vs + i * 512), 16,
-        2 * (lane16 + (i >> 2) * (int)vblk_stride + (i & 3) * 512), 0, 0, 0);
-  };
-  auto zero_v_tail = [&](int t) {
-    _Float16* vs = vbuf0 + (t & 1) * V_TILE_HALVES;
-    for (int b = 0; b < 8; b++) {
-      const int valid = kv_len - (t * BK + 8 * b);
-      if (valid >= 8) continue;
-      _Float16* col8 = vs + (b * D + threadIdx.x) * 8;
-#pragma unroll
-      for (int e = 0; e < 8; e++)
-        if (e >= valid) col8[e] = (_Float16)0.f;
-    }
-  };
-  const bool tail_tile = (kv_len % BK) != 0;
-
-  const int krow = qk_row_key(col);
-  const int k_lds_off =
-      kp * KSUB + ((krow >> 2) & 1) * KU + hl * 128 + (((krow >> 3) << 2) | (krow & 3)) * 8;
-  // V fragment (step s of 16 keys, value block i of 32 columns) of this
-  // wave's key half: 8-key block 4 kp + 2 s + hl of the tile.
-  const int v_lds_off = (4 * kp + hl) * (D * 8) + col * 8;
-  auto vfrag = [&](const _Float16* vs, int idx) {  // idx = 8 s + i
-    return *(const f16x8*)(vs + 2 * (idx >> 3) * (D * 8) + (idx & 7) * 256);
-  };
-
-  // S^T = K . Q^T of this wave's 32-key half of tile t for both column
-  // blocks, with the copies of K(tk) (into tile t + 1's buffer) and, when
-  // with_v, of V(t): one asm block of 32 MFMAs
-  // (the scores must come out in ordinary registers, the compiler would
-  // give every MFMA of the kernel the accumulation-register form), the K
-  // fragments read four k-steps ahead through a ring of four, and one copy
-  // piece issued per k-step (K pieces on even steps, V on odd).  Only the
-  // first tile takes its V copies here; in the steady walk they go into the
-  // PV phase (copy_v_piece), so that QK's LDS port carries the K fragment
-  // reads and the K copies alone.  ka: LDS
-  // byte address of the lane's K fragment 0; mk / mv: LDS byte addresses of
-  // the wave's first K / V piece; vk / vv: the lane's byte offsets in the
-  // source tiles; sv: offset of the wave's second group of four V pieces.
-  // Ends with 16 wait states, since VALU code reads the results next.
-  // (m0 in the clobber list: the compiler sets m0 right before each of its
-  // own LDS copies, so nothing it holds there lives across the block.)
-  // The asm text is a macro; VC(m0 offset, soffset instruction) stands for
-  // the copy of one V piece, or for nothing.
-#define PF_VCOPY(mo, soi) "s_add_u32 m0, %[mv], " #mo "\n" soi "s_nop 0\n" \
-  "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
-#define PF_NOCOPY(mo, soi)
-#define PF_QK_ASM(VC) \
-    "ds_read_b128 %[r0], %[ka] offset:0\n" \
-    "ds_read_b128 %[r1], %[ka] offset:512\n" \
-    "ds_read_b128 %[r2], %[ka] offset:1024\n" \
-    "ds_read_b128 %[r3], %[ka] offset:1536\n" \
-    "s_waitcnt lgkmcnt(3)\n" \
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r0], %[q0_0], 0\n" \
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r0], %[q1_0], 0\n" \
-    "ds_read_b128 %[r0], %[ka] offset:2048\n" \
-    "s_add_u32 m0, %[mk], 0\n" \
-    "s_mov_b32 %[so], 0\n" \
-    "s_nop 0\n" \
-    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n" \
-    "s_waitcnt lgkmcnt(3)\n" \
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r1], %[q0_1], %[c0]\n" \
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r1], %[q1_1], %[c1]\n" \
-    "ds_read_b128 %[r1], %[ka] offset:2560\n" \
-    VC(0, "s_mov_b32 %[so], 0\n") \
-    "s_waitcnt lgkmcnt(3)\n" \
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r2], %[q0_2], %[c0]\n" \
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r2], %[q1_2], %[c1]\n" \
-    "ds_read_b128 %[r2], %[ka] offset:3072\n" \
-    "s_add_u32 m0, %[mk], 1024\n" \
-    "s_movk_i32 %[so], 1024\n" \
-    "s_nop 0\n" \
-    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n" \
-    "s_waitcnt lgkmcnt(3)\n" \
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r3], %[q0_3], %[c0]\n" \
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r3], %[q1_3], %[c1]\n" \
-    "ds_read_b128 %[r3], %[ka] offset:3584\n" \
-    VC(1024, "s_movk_i32 %[so], 1024\n") \
-    "s_waitcnt lgkmcnt(3)\n" \
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r0], %[q0_4], %[c0]\n" \
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r0], %[q1_4], %[c1]\n" \
-    "ds_read_b128 %[r0], %[ka] offset:4096\n" \
-    "s_add_u32 m0, %[mk], 2048\n" \
-    "s_movk_i32 %[so], 2048\n" \
-    "s_nop 0\n" \
-    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n" \
-    "s_waitcnt lgkmcnt(3)\n" \
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r1], %[q0_5], %[c0]\n" \
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r1], %[q1_5], %[c1]\n" \
-    "ds_read_b128 %[r1], %[ka] offset:4608\n" \
-    VC(2048, "s_movk_i32 %[so], 2048\n") \
-    "s_waitcnt lgkmcnt(3)\n" \
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r2], %[q0_6], %[c0]\n" \
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r2], %[q1_6], %[c1]\n" \
-    "ds_read_b128 %[r2], %[ka] offset:5120\n" \
-    "s_add_u32 m0, %[mk], 3072\n" \
-    "s_movk_i32 %[so], 3072\n" \
-    "s_nop 0\n" \
-    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n" \
-    "s_waitcnt lgkmcnt(3)\n" \
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r3], %[q0_7], %[c0]\n" \
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r3], %[q1_7], %[c1]\n" \
-    "ds_read_b128 %[r3], %[ka] offset:5632\n" \
-    VC(3072, "s_movk_i32 %[so], 3072\n") \
-    "s_waitcnt lgkmcnt(3)\n" \
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r0], %[q0_8], %[c0]\n" \
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r0], %[q1_8], %[c1]\n" \
-    "ds_read_b128 %[r0], %[ka] offset:6144\n" \
-    "s_add_u32 m0, %[mk], 4096\n" \
-    "s_movk_i32 %[so], 4096\n" \
-    "s_nop 0\n" \
-    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n" \
-    "s_waitcnt lgkmcnt(3)\n" \
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r1], %[q0_9], %[c0]\n" \
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r1], %[q1_9], %[c1]\n" \
-    "ds_read_b128 %[r1], %[ka] offset:6656\n" \
-    VC(4096, "s_add_u32 %[so], %[sv], 0\n") \
-    "s_waitcnt lgkmcnt(3)\n" \
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r2], %[q0_10], %[c0]\n" \
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r2], %[q1_10], %[c1]\n" \
-    "ds_read_b128 %[r2], %[ka] offset:7168\n" \
-    "s_add_u32 m0, %[mk], 5120\n" \
-    "s_movk_i32 %[so], 5120\n" \
-    "s_nop 0\n" \
-    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n" \
-    "s_waitcnt lgkmcnt(3)\n" \
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r3], %[q0_11], %[c0]\n" \
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r3], %[q1_11], %[c1]\n" \
-    "ds_read_b128 %[r3], %[ka] offset:7680\n" \
-    VC(5120, "s_add_u32 %[so], %[sv], 1024\n") \
-    "s_waitcnt lgkmcnt(3)\n" \
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r0], %[q0_12], %[c0]\n" \
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r0], %[q1_12], %[c1]\n" \
-    "s_add_u32 m0, %[mk], 6144\n" \
-    "s_movk_i32 %[so], 6144\n" \
-    "s_nop 0\n" \
-    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n" \
-    "s_waitcnt lgkmcnt(2)\n" \
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r1], %[q0_13], %[c0]\n" \
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r1], %[q1_13], %[c1]\n" \
-    VC(6144, "s_add_u32 %[so], %[sv], 2048\n") \
-    "s_waitcnt lgkmcnt(1)\n" \
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r2], %[q0_14], %[c0]\n" \
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r2], %[q1_14], %[c1]\n" \
-    "s_add_u32 m0, %[mk], 7168\n" \
-    "s_movk_i32 %[so], 7168\n" \
-    "s_nop 0\n" \
-    "buffer_load_dwordx4 %[vk], %[rk], %[so] offen lds\n" \
-    "s_waitcnt lgkmcnt(0)\n" \
-    "v_mfma_f32_32x32x16_f16 %[c0], %[r3], %[q0_15], %[c0]\n" \
-    "v_mfma_f32_32x32x16_f16 %[c1], %[r3], %[q1_15], %[c1]\n" \
-    VC(7168, "s_add_u32 %[so], %[sv], 3072\n") \
-    "s_nop 15\n"
-#define ASM_OPERANDS \
-  : [c0] "=&v"(c0), [c1] "=&v"(c1), [r0] "=&v"(r0), [r1] "=&v"(r1), [r2] "=&v"(r2), \
-  [r3] "=&v"(r3), [so] "=&s"(so) \
-  : [ka] "v"(ka), [mk] "s"(mk), [mv] "s"(mv), [rk] "s"(rk), [rv] "s"(rv), \
-  [vk] "v"(vk_off), [vv] "v"(vv_off), [sv] "s"(sv_off), \
-  [q0_0] "v"(qf[0][0]), [q0_1] "v"(qf[0][1]), [q0_2] "v"(qf[0][2]), [q0_3] "v"(qf[0][3]), \
-  [q0_4] "v"(qf[0][4]), [q0_5] "v"(qf[0][5]), [q0_6] "v"(qf[0][6]), [q0_7] "v"(qf[0][7]), \
-  [q0_8] "v"(qf[0][8]), [q0_9] "v"(qf[0][9]), [q0_10] "v"(qf[0][10]), [q0_11] "v"(qf[0][11]), \
-  [q0_12] "v"(qf[0][12]), [q0_13] "v"(qf[0][13]), [q0_14] "v"(qf[0][14]), [q0_15] "v"(qf[0][15]), \
-  [q1_0] "v"(qf[1][0]), [q1_1] "v"(qf[1][1]), [q1_2] "v"(qf[1][2]), [q1_3] "v"(qf[1][3]), \
-  [q1_4] "v"(qf[1][4]), [q1_5] "v"(qf[1][5]), [q1_6] "v"(qf[1][6]), [q1_7] "v"(qf[1][7]), \
-  [q1_8] "v"(qf[1][8]), [q1_9] "v"(qf[1][9]), [q1_10] "v"(qf[1][10]), [q1_11] "v"(qf[1][11]), \
-  [q1_12] "v"(qf[1][12]), [q1_13] "v"(qf[1][13]), [q1_14] "v"(qf[1][14]), [q1_15] "v"(qf[1][15]) \
-  : "m0", "memory"
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-  auto qk = [&](int t, int tk, f32x16& c0, f32x16& c1, bool with_v) {
-    const int ka = lds_addr(kbuf0 + (t & 1) * K_TILE_HALVES + k_lds_off);
-    const int mk = __builtin_amdgcn_readfirstlane(k_piece_lds(t + 1));
-    const int mv = __builtin_amdgcn_readfirstlane(v_piece_lds(t));
-    const __amdgpu_buffer_rsrc_t rk = k_tile_src(tk), rv = v_tile_src(t);
-    f16x8 r0, r1, r2, r3;
-    int so;
-    if (with_v)
-      asm volatile(PF_QK_ASM(PF_VCOPY) ASM_OPERANDS);
-    else
-      asm volatile(PF_QK_ASM(PF_NOCOPY) ASM_OPERANDS);
-  };
-  // Copy of V piece pi of tile t (the wave's 8 pieces, as in the asm block),
-  // issued in the first eight slots of the PV phase: V(t) lands in the
-  // buffer PV(t-2) read, which the previous iteration's barrier freed, and
-  // the iteration's closing wait covers it.
-  auto copy_v_piece = [&](int t, int pi) {
-    const int mv = __builtin_amdgcn_readfirstlane(v_piece_lds(t)) + 1024 * pi;
-    const int so = pi < 4 ? 1024 * pi : sv_off + 1024 * (pi - 4);
-    asm volatile(
-        "s_mov_b32 m0, %[mv]\n"
-        "s_nop 0\n"
-        "buffer_load_dwordx4 %[vv], %[rv], %[so] offen lds\n"
-        :
-        : [mv] "s"(mv), [rv] "s"(v_tile_src(t)), [vv] "v"(vv_off), [so] "s"(so)
-        : "m0", "memory");
-  };
-#pragma clang diagnostic pop
-#undef PF_VCOPY
-#undef PF_NOCOPY
-#undef PF_QK_ASM
-#undef ASM_OPERANDS
-  auto tile_max = [&](const f32x16& sc) {
-    float mt = sc[0];
-#pragma unroll
-    for (int e = 1; e < 16; e++) mt = fmaxf(mt, sc[e]);
-    return mi::max_xor32(mt) * c2;
-  };
-  // Weights of one column block against reference max mm into p (f16);
-  // returns the lane's partial row sum.
-  auto weights = [&](const f32x16& sc, float mm, f16x8 (&p)[2]) {
-    float rs = 0.f;
-#pragma unroll
-    for (int e = 0; e < 16; e += 2) {
-      const f16x2 ph = {(_Float16)__builtin_amdgcn_exp2f(fmaf(sc[e], c2, -mm)),
-                        (_Float16)__builtin_amdgcn_exp2f(fmaf(sc[e + 1], c2, -mm))};
-      rs = __builtin_amdgcn_fdot2(ph, f16x2{1.f16, 1.f16}, rs, false);
-      p[e >> 3][e & 7] = ph[0];
-      p[e >> 3][(e & 7) + 1] = ph[1];
-    }
-    return rs;
-  };
-  // Causal mask of a diagonal half tile: key (key0 + 16 (e/8) + 8 hl + e%8)
-  // is visible to query qpos0 + 32 b.
-  auto mask = [&](int t, f32x16& c0, f32x16& c1) {
-    const int key0 = t * BK + 32 * kp;
-#pragma unroll
-    for (int b = 0; b < 2; b++) {
-      const int rel = qpos0 + 32 * b - key0 - 8 * hl;
-      f32x16& sc = b ? c1 : c0;
-#pragma unroll
-      for (int e = 0; e < 16; e++)
-        if (16 * (e >> 3) + (e & 7) > rel) sc[e] = -INFINITY;
-    }
-  };
-  // PV of tile t alone (the wave has no keys in the next tile).
-  f16x8 pprev[2][2];  // P^T of the previous tile: [column block][16-key step]
-  auto pv = [&](int t) {
-    const _Float16* vs = vbuf0 + (t & 1) * V_TILE_HALVES + v_lds_off;
-    constexpr int kR = 4;
-    f16x8 vf[kR];
-#pragma unroll
-    for (int k = 0; k < kR; k++) vf[k] = vfrag(vs, k);
-#pragma unroll
-    for (int idx = 0; idx < 16; idx++) {
-      const int s = idx >> 3, i = idx & 7;
-      acc[0][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[idx % kR], pprev[0][s], acc[0][i], 0, 0, 0);
-      acc[1][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[idx % kR], pprev[1][s], acc[1][i], 0, 0, 0);
-      if (idx + kR < 16) vf[idx % kR] = vfrag(vs, idx + kR);
-    }
-  };
-
-  // The reference max m of a column is fixed for the whole walk: the max
-  // of the wave's first tile, so weights 2^(s - m) are never rescaled and O
-  // needs no rescaling either (every VALU touch of the 256 accumulation
-  // registers would move them out of those registers).  Weights stay in f16
-  // range while no score exceeds m by 15 or more (base 2); if one does, the
-  // workgroup starts over: a max pass (QK only) takes the exact row max
-  // over every visible key, and the walk is redone against it, where no
-  // weight exceeds 1.  Only valid query columns count (padding columns past
-  // n may see stale rows).  Benign data never pays for the restart.
-  const bool valid0 = q0 + 64 * qb + col < a.n, valid1 = q0 + 64 * qb + 32 + col < a.n;
-  int* const ovf_word = (int*)(lds + LDS_FLAG_OFF);  // set by a wave whose weights overflowed
-  bool pending = false;
-  if (threadIdx.x == 0) ovf_word[0] = 0;  // published by tile 0's barrier
-  // The walk over the tiles; against the exact max (after a restart) it
-  // neither checks for nor reports overflow.  Returns whether the workgroup
-  // must start over.
-  auto walk = [&](bool exact) {
-#pragma unroll
-    for (int b = 0; b < 2; b++)
-#pragma unroll
-      for (int i = 0; i < 8; i++) acc[b][i] = f32x16{};
-    // Tile 0: K(0) first, then QK(0) with the copies of K(1) (K(0) again
-    // when it is the only tile) and V(0).
-#pragma unroll
-    for (int pi = 0; pi < 8; pi++) load_k_piece(0, pi);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    {
-      f32x16 c0, c1;
-      qk(0, nt > 1 ? 1 : 0, c0, c1, true);
-      if (mi::prefill64_diag(pw, 0)) mask(0, c0, c1);
-      if (!exact) {  // a column with no visible key keeps kNegBig (weights 0)
-        m[0] = fmaxf(tile_max(c0), kNegBig);
-        m[1] = fmaxf(tile_max(c1), kNegBig);
-      }
-      l[0] = mi::sum_xor32(weights(c0, m[0], pprev[0]));
-      l[1] = mi::sum_xor32(weights(c1, m[1], pprev[1]));
-      pending = true;
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      if (tail_tile && nt == 1) {
-        zero_v_tail(0);
-        __syncthreads();
-      }
-    }
-    for (int t = 1; t < nt; t++) {
-      const int tk = t + 1 < nt ? t + 1 : t;  // K copy source (t + 1, or a repeat)
-      bool ovf = false;
-      if (mi::prefill64_active(pw, t)) {  // implies pending
-        const _Float16* vs = vbuf0 + ((t - 1) & 1) * V_TILE_HALVES + v_lds_off;
-        constexpr int vRing = 4;
-        f32x16 c0, c1;
-        qk(t, tk, c0, c1, false);
-        if (mi::prefill64_diag(pw, t)) mask(t, c0, c1);  // wave-uniform
-        // PV(t-1), with tile t's weights computed between its MFMAs.
-        f16x8 vf[vRing];
-#pragma unroll
-        for (int k = 0; k < vRing; k++) vf[k] = vfrag(vs, k);
-        f16x8 pnew[2][2];
-        float rs0 = 0.f, rs1 = 0.f;
-        // Slot idx: two MFMAs, with the slot's two weights (scores 2 idx,
-        // 2 idx + 1 of the 32) spread around them and pipelined one slot
-        // deep, so that no VALU op waits for the one just before it (a wave
-        // issues in order; after each MFMA about two FMAs and one
-        // exponential issue in its shadow):
-        //   after MFMA 0: exp(a_idx), fma(a_idx+1), cvt(idx-1)
-        //   after MFMA 1: exp(b_idx), fma(b_idx+1), dot2(idx-1)
-        auto score = [&](int j) {  // raw score j of the 32 (block j / 16)
-          const int bb = j >> 4, ee = j & 15;
-          return bb ? c1[ee] : c0[ee];
-        };
-        float ya = fmaf(score(0), c2, -m[0]), yb = fmaf(score(1), c2, -m[0]);
-        float xa_prev = 0.f, xb_prev = 0.f;
-        f16x2 ph_prev = {};
-#pragma unroll
-        for (int idx = 0; idx < 17; idx++) {
-          const int s = idx >> 3, i = idx & 7;
-          if (idx < 16)
-            acc[0][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[idx % vRing], pprev[0][s], acc[0][i], 0, 0, 0);
-          if (idx < 8) copy_v_piece(t, idx);
-          float xa = 0.f, ya_next = 0.f;
-          if (idx < 16) xa = __builtin_amdgcn_exp2f(ya);
-          if (idx < 15) ya_next = fmaf(score(2 * idx + 2), c2, -m[(idx + 1) >> 3]);
-          if (idx > 0) ph_prev = f16x2{(_Float16)xa_prev, (_Float16)xb_prev};
-          __builtin_amdgcn_sched_barrier(0);
-          if (idx < 16) {
-            acc[1][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[idx % vRing], pprev[1][s], acc[1][i], 0, 0, 0);
-            if (idx + vRing < 16) vf[idx % vRing] = vfrag(vs, idx + vRing);
-          }
-          float xb = 0.f, yb_next = 0.f;
-          if (idx < 16) xb = __builtin_amdgcn_exp2f(yb);
-          if (idx < 15) yb_next = fmaf(score(2 * idx + 3), c2, -m[(idx + 1) >> 3]);
-          if (idx > 0) {
-            const int jp = idx - 1, bp = jp >> 3, ep = 2 * (jp & 7);
-            if (bp) rs1 = __builtin_amdgcn_fdot2(ph_prev, f16x2{1.f16, 1.f16}, rs1, false);
-            else rs0 = __builtin_amdgcn_fdot2(ph_prev, f16x2{1.f16, 1.f16}, rs0, false);
-            pnew[bp][ep >> 3][ep & 7] = ph_prev[0];
-            pnew[bp][ep >> 3][(ep & 7) + 1] = ph_prev[1];
-          }
-          xa_prev = xa;
-          xb_prev = xb;
-          ya = ya_next;
-          yb = yb_next;
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        // a weight of 2^15 or more (each is at most its lane's sum) leaves
-        // f16 range; also inf / NaN
-        ovf = (valid0 && !(rs0 < 32768.f)) || (valid1 && !(rs1 < 32768.f));
-        l[0] += mi::sum_xor32(rs0);
-        l[1] += mi::sum_xor32(rs1);
-#pragma unroll
-        for (int b = 0; b < 2; b++)
-#pragma unroll
-          for (int s = 0; s < 2; s++) pprev[b][s] = pnew[b][s];
-        pending = true;
-      } else {
-        if (t + 1 < nt) {
-#pragma unroll
-          for (int pi = 0; pi < 8; pi++) load_k_piece(t + 1, pi);
-        }
-#pragma unroll
-        for (int pi = 0; pi < 8; pi++) load_v_piece(t, pi);
-        if (pending) pv(t - 1);
-        pending = false;
-      }
-      if (!exact && __ballot(ovf)) ovf_word[0] = 1;
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      if (tail_tile && t + 1 == nt) {
-        zero_v_tail(t);
-        __syncthreads();
-      }
-    }
-    // read after the last barrier: the same for every wave
-    return !exact && ovf_word[0] != 0;
-  };
-  if (walk(false)) {
-    // Max pass: every tile's QK, masked, folded into m (no V copies).
-    __syncthreads();  // every wave has read the flag word
-    m[0] = m[1] = kNegBig;
-#pragma unroll
-    for (int pi = 0; pi < 8; pi++) load_k_piece(0, pi);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int t = 0; t < nt; t++) {
-      const int tk = t + 1 < nt ? t + 1 : t;
-      if (mi::prefill64_active(pw, t)) {
-        f32x16 c0, c1;
-        qk(t, tk, c0, c1, false);
-        if (mi::prefill64_diag(pw, t)) mask(t, c0, c1);
-        m[0] = fmaxf(m[0], tile_max(c0));
-        m[1] = fmaxf(m[1], tile_max(c1));
-      } else if (t + 1 < nt) {
-#pragma unroll
-        for (int pi = 0; pi < 8; pi++) load_k_piece(t + 1, pi);
-      }
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-    }
-    walk(true);
-  }
-  if (pending) pv(nt - 1);
-
-  // Merge of the two key halves: wave (qb, kp) finishes query half kp of
-  // rows qb (column block kp) and hands the other block to its partner
-  // through LDS.  The wave of key half 1 first swaps its two blocks (and
-  // their (m, l)), so that from here on block 0 is the one finished and
-  // block 1 the one handed over in every wave: the code below names fixed
-  // accumulation registers (a block index that differed by wave would turn
-  // every accumulator access into a select, and a block named at compile
-  // time in two copies of this code left the compiler copying all 256 out
-  // of the accumulation registers, with spills).  Region (qb, h) holds
-  // 32 KiB of O^T of query half h (lane-contiguous 16-byte pieces) and the
-  // (m, l) pairs.  Every long-latency access
-  // of the epilogue is issued in one batch: the gate rows before the
-  // hand-over (their global latency overlaps it), the partner's 32 pieces
-  // in two batches of 16 right after it (in registers Q^T held), so that no
-  // access waits for the one before it.
-  __syncthreads();  // every wave is done with the K/V tiles
-  if (__builtin_amdgcn_readfirstlane(kp)) {
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const f32x16 t = acc[0][i];
-      acc[0][i] = acc[1][i];
-      acc[1][i] = t;
-    }
-    const float tm = m[0], tl = l[0];
-    m[0] = m[1]; l[0] = l[1]; m[1] = tm; l[1] = tl;
-  }
-  float* const rgn = (float*)lds;                   // [2][2][8*4][64][4]
-  float* const mlr = rgn + 2 * 2 * 8 * 4 * 64 * 4;  // [2][2][32][2]
-  auto finish = [&](auto GATED) {
-    constexpr int ob = 0, gb = 1;
-    constexpr bool gated = decltype(GATED)::value;
-    const int qo = q0 + 64 * qb + 32 * kp + col;
-    const bool qvalid = qo < a.n;
-    // Output: lane (col, hl) holds columns 32 i + 8 g + 4 hl .. + 3 of
-    // query qo; a v_permlane32_swap between the two lane halves gives lane
-    // hl all eight columns of chunk (i, g = 2 j + hl), so every lane writes
-    // whole 16-byte chunks (half the store instructions of 8-byte pieces).
-    _Float16* op = a.out + ((int64_t)qo * a.H + hq) * D;
-    f16x8 gv[16];
-    if constexpr (gated) {
-      const _Float16* gp = a.gate + ((int64_t)(qvalid ? qo : 0) * a.H + hq) * D;
-#pragma unroll
-      for (int i = 0; i < 8; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) gv[2 * i + j] = *(const f16x8*)(gp + 32 * i + 8 * (2 * j + hl));
-    }
-    float* dst = rgn + (qb * 2 + 1 - kp) * (8 * 4 * 64 * 4);
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-#pragma unroll
-      for (int e4 = 0; e4 < 4; e4++) {
-        f32x4 o = {acc[gb][i][4 * e4], acc[gb][i][4 * e4 + 1], acc[gb][i][4 * e4 + 2],
-                   acc[gb][i][4 * e4 + 3]};
-        *(f32x4*)(dst + ((i * 4 + e4) * 64 + lane) * 4) = o;
-      }
-    if (hl == 0) {
-      float* mdst = mlr + ((qb * 2 + 1 - kp) * 32 + col) * 2;
-      mdst[0] = m[gb];
-      mdst[1] = l[gb];
-    }
-    mi::sync_lds();
-    const float* src = rgn + (qb * 2 + kp) * (8 * 4 * 64 * 4);
-    const float* msrc = mlr + ((qb * 2 + kp) * 32 + col) * 2;
-    const float mo = msrc[0], lo = msrc[1];
-    const float M = fmaxf(m[ob], mo);
-    const float sw = __builtin_amdgcn_exp2f(m[ob] - M), so = __builtin_amdgcn_exp2f(mo - M);
-    const float L = l[ob] * sw + lo * so;
-    const float inv = (L > 0.f) ? 1.f / L : 0.f;
-    const float fw = sw * inv, fo = so * inv;
-    auto swap32 = [](float& lo, float& hi) {  // lo of the upper half <-> hi of the lower half
-      auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
-      lo = __uint_as_float(r[0]);
-      hi = __uint_as_float(r[1]);
-    };
-    // the partner's pieces in two batches of 16 (64 registers each)
-    f32x4 x[16];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      if (i % 4 == 0) {
-#pragma unroll
-        for (int p = 0; p < 16; p++) x[p] = *(const f32x4*)(src + ((i * 4 + p) * 64 + lane) * 4);
-      }
-      // one column chunk at a time (keeps the accumulator copies short-lived)
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int j = 0; j < 2; j++) {
-        // y[k][e]: value e of chunk (i, 2 j + k) held by this lane
-        float y[2][4];
-#pragma unroll
-        for (int k = 0; k < 2; k++) {
-          const int g4 = 2 * j + k;
-#pragma unroll
-          for (int e = 0; e < 4; e++) y[k][e] = acc[ob][i][4 * g4 + e] * fw + x[(i % 4) * 4 + g4][e] * fo;
-        }
-        // lane half 0 keeps chunk 2j (its columns 0..3, receives 4..7);
-        // lane half 1 keeps chunk 2j + 1 (receives 0..3, its 4..7)
-#pragma unroll
-        for (int e = 0; e < 4; e++) swap32(y[0][e], y[1][e]);
-        // now lane half 0: y[0] = columns 0..3, y[1] = 4..7 of chunk 2j;
-        // lane half 1: y[0] = columns 0..3, y[1] = 4..7 of chunk 2j + 1
-        const int cofs = 32 * i + 8 * (2 * j + hl);
-        f16x8 h;
-        if constexpr (gated) {
-          const f16x8 g = gv[2 * i + j];
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            h[e] = (_Float16)mi::gate_mul(y[0][e], (float)g[e]);
-            h[4 + e] = (_Float16)mi::gate_mul(y[1][e], (float)g[4 + e]);
-          }
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            h[e] = (_Float16)y[0][e];
-            h[4 + e] = (_Float16)y[1][e];
-          }
-        }
-        if (qvalid) *(f16x8*)(op + cofs) = h;
-      }
-    }
-  };
-  if (a.gate) finish(std::true_type{});
-  else finish(std::false_type{});
+// Launches attn_prefill64_kernel (prefill) or attn_verify_wide_kernel
+// (`grid` workgroups of 256 threads).
+mi_status launch_prefill64(const PrefillArgs& a, int grid, hipStream_t s) {
+  static std::atomic<uint64_t> lds_set{0};
+  MI_TRY(mi::set_lds_limit((const void*)attn_prefill64_kernel, LDS64_BYTES, lds_set));
+  MI_HIP(mi::launch("attn_prefill", attn_prefill64_kernel, dim3(grid), dim3(256),
+                    (size_t)LDS64_BYTES, s, a));
+  return MI_OK;
+}
+mi_status launch_verify_wide(const PrefillArgs& a, const VerifyArgs& v, int grid,
+                             hipStream_t s) {
+  static std::atomic<uint64_t> lds_set{0};
+  MI_TRY(mi::set_lds_limit((const void*)attn_verify_wide_kernel, LDS64_BYTES, lds_set));
+  MI_HIP(mi::launch("verify_wide", attn_verify_wide_kernel, dim3(grid), dim3(256),
+                    (size_t)LDS64_BYTES, s, a, v));
+  return MI_OK;
 }
 
 // Queries per wave of the prefill kernel: 64 (attn_prefill64_kernel, the
@@ -1162,6 +588,36 @@ int prefill_qpw() {
 }
 
 }  // namespace
+
+namespace mi {
+
+mi_status verify_wide_split(const mi_kv* kv, int32_t layer, const _Float16* q, int64_t past,
+                            int32_t n, int64_t chunk, int32_t nchunks, float* part_o,
+                            float* part_ml, hipStream_t stream) {
+  if (n <= 0 || n > BQ / 8 || chunk <= 0 || chunk % BK != 0 || nchunks <= 0 ||
+      (int64_t)nchunks * chunk < past + n || past + n + 2 * BK >= ((int64_t)1 << 31))
+    return fail(MI_ERR_INVALID_ARG, "verify split: n=%d chunk=%lld nchunks=%d past=%lld", n,
+                (long long)chunk, nchunks, (long long)past);
+  PrefillArgs a{};
+  a.q = q;
+  a.k = kv->k[layer];
+  a.v = kv->v[layer];
+  a.past = past;
+  a.n = n;
+  a.H = kv->H;
+  a.G = kv->G;
+  a.scale_log2e = kLog2e / sqrtf((float)D);
+  VerifyArgs vx{};
+  vx.chunk = chunk;
+  vx.nchunks = nchunks;
+  vx.ncols = 8 * n;
+  vx.nslots = nchunks;
+  vx.part_o = part_o;
+  vx.part_ml = part_ml;
+  return launch_verify_wide(a, vx, nchunks * kv->G, stream);
+}
+
+}  // namespace mi
 
 extern "C" mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
                                      const mi_f16* k, const mi_f16* v, const mi_f16* gate,
@@ -1206,10 +662,7 @@ extern "C" mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
                 "attn_prefill64_kernel's merge area lies below its restart flag");
   const int grid = (a.work + 63) / 64 * 64;
   if (prefill_qpw() == 64) {
-    static std::atomic<uint64_t> lds_set64{0};
-    MI_TRY(mi::set_lds_limit((const void*)attn_prefill64_kernel, LDS64_BYTES, lds_set64));
-    MI_HIP(mi::launch("attn_prefill", attn_prefill64_kernel, dim3(grid), dim3(256),
-                      (size_t)LDS64_BYTES, s, a));
+    MI_TRY(launch_prefill64(a, grid, s));
   } else {
     static std::atomic<uint64_t> lds_set{0};
     MI_TRY(mi::set_lds_limit((const void*)attn_prefill_kernel, (int)lds, lds_set));

@@ -109,7 +109,8 @@ def test_engine_step_sequence():
 
 
 @pytest.mark.parametrize("n,past", [(1, 0), (2, 5), (3, 31), (4, 61), (4, 255), (7, 100),
-                                    (9, 1000), (6, 20000)])
+                                    (9, 1000), (6, 20000), (16, 0), (5, 59), (16, 61),
+                                    (13, 4093), (12, 4096), (16, 20000)])
 def test_verify_matches_causal_oracle(n, past):
     announce(f"verify n={n} past={past}")
     rng = np.random.default_rng(1000 * n + past)
@@ -120,6 +121,41 @@ def test_verify_matches_causal_oracle(n, past):
     ref = O.causal(q, np.concatenate([kp, k]), np.concatenate([vp, v]), past, gate=g)
     assert_close(out, ref, f"verify n={n} past={past}")
     assert c.len(0) == past + n
+
+
+@pytest.mark.parametrize("n,past", [(16, 20000), (8, 20000)])
+def test_wide_verify_rising_scores_and_grouped_form(n, past, monkeypatch):
+    """5..16 tokens run the wide verify (the prefill's MFMA tiles over key
+    chunks of a few 64-key tiles).  Keys whose scores rise steeply along the
+    context put a chunk's later tiles far above its first tile's max (the
+    fixed reference max), so the workgroups take the restart path; the
+    result matches the oracle and the grouped 4-token form
+    (MI_ATTN_VERIFY_WIDE=0)."""
+    announce(f"wide verify rising n={n} past={past}")
+    rng = np.random.default_rng(n + past)
+    L = past + n
+    q = f16(rng, n, H, D)
+    qdir = q[0].astype(np.float32).reshape(G, 8, D)[:, 0]  # token 0, head 0 of each group
+    qdir /= np.linalg.norm(qdir, axis=-1, keepdims=True)
+    # for those rows, odd 64-key tiles score ~30 (base 2) above even ones: a
+    # chunk that starts on an even tile meets keys far above its first
+    # tile's max
+    ramp = ((np.arange(L) // 64) % 2).astype(np.float32)[:, None, None] * 21.0
+    kall = (0.3 * rng.standard_normal((L, G, D)).astype(np.float32) + ramp * qdir[None])
+    kall = kall.astype(np.float16).reshape(L, G * D)
+    vall = f16(rng, L, G * D)
+    g = f16(rng, n, H, D)
+    # scores (base 2) of the first row: odd tiles far above even ones
+    s2 = (kall[:, :D].astype(np.float32) @ q[0, 0].astype(np.float32)) / 16 * 1.4427
+    assert s2[64:128].min() - s2[:64].max() > 15
+    c = filled_cache(kall[:past], vall[:past], capacity=L)
+    out = attn_verify(c, 0, dev(q), dev(kall[past:]), dev(vall[past:]), past, gate=dev(g))
+    ref = O.causal(q, kall, vall, past, gate=g)
+    assert_close(out, ref, f"wide verify rising n={n}")
+    monkeypatch.setenv("MI_ATTN_VERIFY_WIDE", "0")
+    c.set_pos(past)
+    grouped = attn_verify(c, 0, dev(q), dev(kall[past:]), dev(vall[past:]), past, gate=dev(g))
+    assert_close(grouped, ref, f"grouped verify rising n={n}")
 
 
 def test_verify_c5_and_rollback():
