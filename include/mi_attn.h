@@ -176,7 +176,12 @@ mi_status mi_attn_step(mi_kv* kv, int32_t layer, const mi_f16* q,
  * batched.rs:233-260; kernels kv_cache_append_n + attn_sdpa_causal_n,
  * shaders.metal:2656-2792): append n rows k, v [n][G*D] at past_pos, then
  * query i (q [n][H][D]) attends rows [0, past_pos + i] inclusive; gate
- * [n][H][D] or NULL; out [n][H][D].  MFMA flash-attention kernel.
+ * [n][H][D] or NULL; out [n][H][D].  MFMA flash-attention kernel; up to
+ * 1024 new tokens after a past of at least 4096 rows (and twice n) run its
+ * split-K form over key chunks plus a merge, which needs the handle's
+ * workspace (grown on demand; under graph capture only when it already
+ * suffices, else the unsplit kernel runs).  MI_ATTN_PREFILL_SPLIT=0 turns
+ * the split-K form off.
  * k = v = NULL: rows [past_pos, past_pos+n) are already in the cache (written
  * by mi_qk_norm_rope_append or mi_kv_append; len(layer) >= past_pos + n), no
  * append; len(layer) becomes past_pos + n. */
@@ -187,10 +192,10 @@ mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
 
 /* K-token verify for speculative decoding: same contract as mi_attn_prefill
  * (append at past_pos, query i attends [0, past_pos + i]) for small n, run
- * split-K over the cache: up to 4 tokens in the decode kernel's form, 5..16
- * tokens in one pass of the prefill's MFMA tiles over key chunks that reads
- * each K/V tile once for all tokens (MI_ATTN_VERIFY_WIDE=0 runs them as
- * 4-token groups instead), then a merge.  Rollback afterwards is
+ * split-K over the cache: up to 4 tokens in the decode kernel's form, more
+ * in one pass of the prefill's MFMA tiles over key chunks that reads each
+ * K/V tile once per 16 tokens (MI_ATTN_VERIFY_WIDE=0 runs them as 4-token
+ * groups instead), then a merge.  Rollback afterwards is
  * mi_kv_set_pos.  k = v = NULL as for mi_attn_prefill. */
 mi_status mi_attn_verify(mi_kv* kv, int32_t layer, const mi_f16* q,
                          const mi_f16* k, const mi_f16* v, const mi_f16* gate,

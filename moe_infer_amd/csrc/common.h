@@ -191,14 +191,22 @@ size_t merge_state_bytes(int G);
 // Whether workgroup b of a launch runs on XCD b % 8 on the current device,
 // checked once per device with a probe kernel (decode.hip).
 bool xcd_round_robin();
-// The wide verify's split pass (prefill.hip): attn_prefill64_kernel in its
-// verify form over `nchunks` chunks of `chunk` keys (a multiple of 64) of
-// rows [0, past + n) of `layer`, n <= 16 query tokens q [n][H][D]; writes
-// the unnormalised partials part_o [G][nchunks][8 n][D] and part_ml
-// [G][nchunks][8 n][2] that attn_combine_kernel merges.
+// The wide verify's split pass (prefill.hip): the 64-query prefill body in
+// its split-K form over `nchunks` chunks of `chunk` keys (a multiple of 64)
+// of rows [0, past + n) of `layer`, for the n query tokens q [n][H][D] in
+// row blocks of 16 tokens; writes the unnormalised partials part_o
+// [G][nchunks][8 n][D] and part_ml [G][nchunks][8 n][2] that
+// attn_combine_kernel merges.
 mi_status verify_wide_split(const mi_kv* kv, int32_t layer, const _Float16* q, int64_t past,
                             int32_t n, int64_t chunk, int32_t nchunks, float* part_o,
                             float* part_ml, hipStream_t stream);
+// Causal attention of n query tokens over rows [0, past + n) of `layer`
+// (already in the cache) through the wide verify: the split pass above and
+// the merge (decode.hip).  out [n][H][D], optional gate [n][H][D].
+mi_status attend_wide(mi_kv* kv, int32_t layer, const _Float16* q, const _Float16* gate,
+                      _Float16* out, int64_t past, int32_t n, hipStream_t stream);
+// Workspace bytes attend_wide needs for these sizes.
+size_t wide_workspace_bytes(int G, int64_t past, int32_t n);
 // Enqueues the row copy of kv_cache_append_n on `stream` (no len update).
 mi_status kv_append_rows(mi_kv* kv, int32_t layer, const _Float16* k,
                          const _Float16* v, int64_t pos, int32_t n,

@@ -1242,13 +1242,35 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
 // With k_new / v_new, the n new rows [past_pos, past_pos + n) are appended
 // by the split kernels themselves (each token group appends its own rows,
 // which precede every read of them); the caller has grown the cache.
-// Wide verify for 5..16 query tokens (MI_ATTN_VERIFY_WIDE=0, read at each
-// call, turns it off): one split pass that reads every K/V tile once for all
-// tokens (attn_prefill64_kernel's MFMA tiles over key chunks), then the
-// combine, instead of one split-K launch pair per 4-token group.
+// Wide verify for more than 4 query tokens (MI_ATTN_VERIFY_WIDE=0, read at
+// each call, turns it off): one split pass that reads every K/V tile once
+// per 16 tokens (attn_prefill64_kernel's MFMA tiles over key chunks), then
+// the combine, instead of one split-K launch pair per 4-token group.
 bool verify_wide_enabled() {
   const char* e = getenv("MI_ATTN_VERIFY_WIDE");
   return !(e && *e && atoi(e) == 0);
+}
+
+// Chunking of the wide verify: about 256 workgroups of (row block of 16
+// tokens, chunk, KV head); whole 64-key tiles; at most kMaxChunks chunks
+// (the combine's limit).
+struct WidePlan {
+  int64_t chunk;
+  int nchunks;
+  size_t ws_bytes;  // partials (O, m, l)
+};
+WidePlan wide_plan(int G, int64_t past, int32_t n) {
+  const int64_t rows = past + n;
+  const int nrb = (n + 15) / 16;
+  const int64_t target = std::max<int64_t>(1, (256 + (int64_t)G * nrb - 1) / ((int64_t)G * nrb));
+  int64_t chunk = (rows + target - 1) / target;
+  chunk = std::max<int64_t>(chunk, (rows + kMaxChunks - 1) / kMaxChunks);
+  chunk = (chunk + 63) / 64 * 64;
+  WidePlan p;
+  p.chunk = chunk;
+  p.nchunks = (int)((rows + chunk - 1) / chunk);
+  p.ws_bytes = (size_t)G * p.nchunks * 8 * n * (D + 2) * sizeof(float) + 256;
+  return p;
 }
 
 mi_status wide_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float16* gate,
@@ -1256,16 +1278,13 @@ mi_status wide_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float1
                       const _Float16* k_new, const _Float16* v_new) {
   const int G = kv->G;
   const int64_t rows = past_pos + n;
-  // about 256 workgroups of (chunk, KV head); whole 64-key tiles; at most
-  // kMaxChunks chunks (the combine's limit)
-  int64_t chunk = (rows * G + 255) / 256;
-  chunk = std::max<int64_t>(chunk, (rows + kMaxChunks - 1) / kMaxChunks);
-  chunk = (chunk + 63) / 64 * 64;
-  const int nchunks = (int)((rows + chunk - 1) / chunk);
+  const WidePlan wp = wide_plan(G, past_pos, n);
+  const int64_t chunk = wp.chunk;
+  const int nchunks = wp.nchunks;
   const int ncols = 8 * n;
   const size_t units = (size_t)G * nchunks * ncols;
   void* ws;
-  MI_TRY(mi::kv_workspace(kv, units * (D + 2) * sizeof(float) + 256, stream, &ws));
+  MI_TRY(mi::kv_workspace(kv, wp.ws_bytes, stream, &ws));
   float* part_o = (float*)ws;
   float* part_ml = part_o + units * D;
   if (k_new) MI_TRY(mi::kv_append_rows(kv, layer, k_new, v_new, past_pos, n, stream));
@@ -1292,7 +1311,7 @@ mi_status wide_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float1
 mi_status cache_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float16* gate,
                        _Float16* out, int64_t past_pos, int32_t n, hipStream_t stream,
                        const _Float16* k_new = nullptr, const _Float16* v_new = nullptr) {
-  if (n > 4 && n <= 16 && verify_wide_enabled())
+  if (n > 4 && verify_wide_enabled())
     return wide_attend(kv, layer, q, gate, out, past_pos, n, stream, k_new, v_new);
   const int64_t lim0 = past_pos + 1;
   // The workspace is grown once, to the largest group's need, before any
@@ -1367,6 +1386,13 @@ mi_status attend_cache(mi_kv* kv, int32_t layer, const _Float16* q, const _Float
                        _Float16* out, int64_t past_pos, int32_t n, hipStream_t stream) {
   return cache_attend(kv, layer, q, gate, out, past_pos, n, stream);
 }
+
+mi_status attend_wide(mi_kv* kv, int32_t layer, const _Float16* q, const _Float16* gate,
+                      _Float16* out, int64_t past, int32_t n, hipStream_t stream) {
+  return wide_attend(kv, layer, q, gate, out, past, n, stream, nullptr, nullptr);
+}
+
+size_t wide_workspace_bytes(int G, int64_t past, int32_t n) { return wide_plan(G, past, n).ws_bytes; }
 }  // namespace mi
 
 extern "C" mi_status mi_attn_decode(mi_kv* kv, int32_t layer, const mi_f16* q,

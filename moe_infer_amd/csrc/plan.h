@@ -80,16 +80,21 @@ MI_HD inline PrefillWave64 prefill_wave64(int past, int n, int qtile, int qb, in
   return p;
 }
 // The wide verify's form of the same: the workgroup's keys are chunk
-// [kbeg, kbeg + chunk) of [0, past + n), positions relative to kbeg; rows
-// 64 qb .. + 63 are tokens 8 qb .. 8 qb + 7 (each with the group's eight
-// heads), token i seeing keys up to past + i.
+// [kbeg, kbeg + chunk) of [0, past + n), positions relative to kbeg; its
+// row block holds tokens tok0 .. tok0 + 15, rows 64 qb .. + 63 being tokens
+// tok0 + 8 qb .. + 7 (each with the group's eight heads), token i seeing
+// keys up to past + i.  A chunk past every key its tokens see keeps one
+// tile, fully masked (empty partials).
 MI_HD inline PrefillWave64 verify_wave64(int64_t past, int n, int64_t kbeg, int64_t chunk,
-                                         int qb, int kp) {
+                                         int tok0, int qb, int kp) {
   PrefillWave64 p;
-  p.first = (int)(past - kbeg) + 8 * qb;
+  p.first = (int)(past - kbeg) + tok0 + 8 * qb;
   p.last = p.first + 7;
-  const int64_t end = past + n - kbeg;
-  p.kv_len = (int)(end < chunk ? end : chunk);
+  const int tend = n < tok0 + 16 ? n : tok0 + 16;  // the block's tokens
+  int64_t end = past + tend - kbeg;                 // keys they see in the chunk
+  if (end > chunk) end = chunk;
+  if (end < 1) end = 1;
+  p.kv_len = (int)end;
   p.nt = (p.kv_len + kPrefillBK - 1) / kPrefillBK;
   p.koff = 32 * kp;
   return p;

@@ -579,6 +579,17 @@ mi_status launch_verify_wide(const PrefillArgs& a, const VerifyArgs& v, int grid
   return MI_OK;
 }
 
+// Whether mi_attn_prefill takes the split-K form (the wide verify's pass and
+// merge): up to 1024 new tokens after a past of at least 4096 rows and
+// twice the new tokens.  Timed at past 65536: 16 / 128 / 512 new tokens
+// took 1434 / 1446 / 1455 us as the prefill grid.  MI_ATTN_PREFILL_SPLIT=0
+// (read at each call) turns it off.
+bool prefill_split_k(int64_t past, int32_t n) {
+  const char* e = getenv("MI_ATTN_PREFILL_SPLIT");
+  if (e && *e && atoi(e) == 0) return false;
+  return n <= 1024 && past >= 4096 && past >= 2 * (int64_t)n;
+}
+
 // Queries per wave of the prefill kernel: 64 (attn_prefill64_kernel, the
 // default) or 32 (attn_prefill_kernel, MI_ATTN_PREFILL_QPW=32: the earlier
 // form, kept for comparison).  Read at each call.
@@ -594,8 +605,10 @@ namespace mi {
 mi_status verify_wide_split(const mi_kv* kv, int32_t layer, const _Float16* q, int64_t past,
                             int32_t n, int64_t chunk, int32_t nchunks, float* part_o,
                             float* part_ml, hipStream_t stream) {
-  if (n <= 0 || n > BQ / 8 || chunk <= 0 || chunk % BK != 0 || nchunks <= 0 ||
-      (int64_t)nchunks * chunk < past + n || past + n + 2 * BK >= ((int64_t)1 << 31))
+  const int nrb = (n + 15) / 16;  // row blocks of 16 tokens
+  if (n <= 0 || chunk <= 0 || chunk % BK != 0 || nchunks <= 0 ||
+      (int64_t)nchunks * chunk < past + n || past + n + 2 * BK >= ((int64_t)1 << 31) ||
+      (int64_t)nrb * nchunks * kv->G >= ((int64_t)1 << 31))
     return fail(MI_ERR_INVALID_ARG, "verify split: n=%d chunk=%lld nchunks=%d past=%lld", n,
                 (long long)chunk, nchunks, (long long)past);
   PrefillArgs a{};
@@ -614,7 +627,7 @@ mi_status verify_wide_split(const mi_kv* kv, int32_t layer, const _Float16* q, i
   vx.nslots = nchunks;
   vx.part_o = part_o;
   vx.part_ml = part_ml;
-  return launch_verify_wide(a, vx, nchunks * kv->G, stream);
+  return launch_verify_wide(a, vx, nrb * nchunks * kv->G, stream);
 }
 
 }  // namespace mi
@@ -644,6 +657,20 @@ extern "C" mi_status mi_attn_prefill(mi_kv* kv, int32_t layer, const mi_f16* q,
     kv->len[layer] = past_pos + n;
   }
   hipStream_t s = (hipStream_t)stream;
+  // A few tokens after a long past: the prefill grid (one workgroup per 128
+  // queries and head) would leave most CUs idle while each of its
+  // workgroups walks the whole past; the split-K form of the same tiles
+  // spreads the past over the CUs, then merges.  Not while a graph is being
+  // captured unless the workspace already suffices (growing it is refused
+  // then).
+  if (prefill_split_k(past_pos, n)) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    MI_HIP(hipStreamIsCapturing(s, &cs));
+    if (cs == hipStreamCaptureStatusNone ||
+        kv->ws_bytes >= mi::wide_workspace_bytes(kv->G, past_pos, n))
+      return mi::attend_wide(kv, layer, (const _Float16*)q, (const _Float16*)gate,
+                             (_Float16*)out, past_pos, n, s);
+  }
   PrefillArgs a;
   a.q = (const _Float16*)q;
   a.k = kv->k[layer];

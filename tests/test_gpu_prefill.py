@@ -182,3 +182,54 @@ def test_prefill_restart_after_late_large_scores():
     assert np.all(np.isfinite(out))
     for i in [0, 299, 300, 301, 383, 384, 450, 511, 512, 640, 699]:
         assert_close(out[i], O.decode(q[i].ravel(), k, v, i + 1), f"late large scores row {i}")
+
+
+@pytest.mark.parametrize("past,n", [(4096, 17), (5000, 100), (8192, 1024), (20000, 5),
+                                    (9000, 33)])
+def test_prefill_split_k_form(past, n, monkeypatch):
+    """Up to 1024 new tokens after a past of 4096 rows or more run the
+    split-K form (the prefill tiles over key chunks, row blocks of 16 tokens,
+    then the merge): sampled rows against the oracle, every row against the
+    unsplit kernel (MI_ATTN_PREFILL_SPLIT=0)."""
+    import torch
+    from moe_infer_amd import kv_cache_append
+    announce(f"prefill split-K past={past} n={n}")
+    rng = np.random.default_rng(past + 3 * n)
+    gen = torch.Generator(device="cuda").manual_seed(past + 11 * n)
+    c = Cache(num_layers=1, capacity=past + n)
+    kp = torch.randn(past, G * D, generator=gen, device="cuda").half()
+    vp = torch.randn(past, G * D, generator=gen, device="cuda").half()
+    kv_cache_append(c, 0, kp, vp, 0)
+    c.set_pos(past)
+    q, k, v, g = f16(rng, n, H, D), f16(rng, n, G * D), f16(rng, n, G * D), f16(rng, n, H, D)
+    out = host(attn_prefill(c, 0, dev(q), dev(k), dev(v), past, gate=dev(g)))
+    kall, vall = c.download(0, rows=past + n)
+    for i in sorted({0, 1, 15, 16, n // 2, n - 1}):
+        if i < n:
+            ref = O.decode(q[i].ravel(), kall, vall, past + i + 1, gate=g[i].ravel())
+            assert_close(out[i], ref, f"split-K prefill past={past} n={n} row {i}")
+    monkeypatch.setenv("MI_ATTN_PREFILL_SPLIT", "0")
+    c.set_pos(past)
+    whole = host(attn_prefill(c, 0, dev(q), dev(k), dev(v), past, gate=dev(g)))
+    assert_close(out, whole, f"split-K vs unsplit past={past} n={n}", atol=1e-3)
+
+
+def test_prefill_split_k_restart():
+    """Scores of odd 64-key tiles far above even ones for some rows: chunks
+    whose first tile is even take the restart path in the split-K form."""
+    announce("prefill split-K restart")
+    rng = np.random.default_rng(77)
+    past, n = 12000, 40
+    L = past + n
+    q = f16(rng, n, H, D)
+    qdir = q[0].astype(np.float32).reshape(G, 8, D)[:, 0]
+    qdir /= np.linalg.norm(qdir, axis=-1, keepdims=True)
+    ramp = ((np.arange(L) // 64) % 2).astype(np.float32)[:, None, None] * 21.0
+    kall = (0.3 * rng.standard_normal((L, G, D)).astype(np.float32) + ramp * qdir[None])
+    kall = kall.astype(np.float16).reshape(L, G * D)
+    vall = f16(rng, L, G * D)
+    c = Cache(num_layers=1, capacity=L)
+    c.upload(0, kall[:past], vall[:past])
+    c.set_pos(past)
+    out = attn_prefill(c, 0, dev(q), dev(kall[past:]), dev(vall[past:]), past)
+    assert_close(out, O.causal(q, kall, vall, past), "split-K prefill restart")
