@@ -177,7 +177,7 @@ mi_status mi_attn_step(mi_kv* kv, int32_t layer, const mi_f16* q,
  * shaders.metal:2656-2792): append n rows k, v [n][G*D] at past_pos, then
  * query i (q [n][H][D]) attends rows [0, past_pos + i] inclusive; gate
  * [n][H][D] or NULL; out [n][H][D].  MFMA flash-attention kernel; up to
- * 1024 new tokens after a past of at least 4096 rows (and twice n) run its
+ * 1024 new tokens after a past of at least 2048 rows (and twice n) run its
  * split-K form over key chunks plus a merge, which needs the handle's
  * workspace (grown on demand; under graph capture only when it already
  * suffices, else the unsplit kernel runs).  MI_ATTN_PREFILL_SPLIT=0 turns

@@ -1242,6 +1242,47 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
 // With k_new / v_new, the n new rows [past_pos, past_pos + n) are appended
 // by the split kernels themselves (each token group appends its own rows,
 // which precede every read of them); the caller has grown the cache.
+// Merge of a few chunks (at most kColsChunks) for many columns: one thread
+// per output value, one workgroup of D threads per (column, KV head).  The
+// wide verify's partials for many tokens come in few chunks, where
+// attn_combine_kernel's workgroup per column and 32-value slice (chunks
+// spread over its threads) would launch 16 workgroups per column.
+constexpr int kColsChunks = 16;
+__global__ void __launch_bounds__(D) attn_combine_cols_kernel(CombineArgs a) {
+  const int c = blockIdx.x, kvh = blockIdx.y, d = threadIdx.x;
+  const int ncols = a.nq * 8;
+  const int nch = (int)((a.kv_len + a.chunk - 1) / a.chunk);
+  float m[kColsChunks], l[kColsChunks], o[kColsChunks];
+#pragma unroll
+  for (int ch = 0; ch < kColsChunks; ch++) {
+    m[ch] = kNegBig;
+    l[ch] = 0.f;
+    o[ch] = 0.f;
+    if (ch < nch) {
+      const int64_t slot = ((int64_t)kvh * a.nslots + ch) * ncols + c;
+      m[ch] = a.part_ml[slot * 2];
+      l[ch] = a.part_ml[slot * 2 + 1];
+      o[ch] = a.part_o[slot * D + d];
+    }
+  }
+  float M = kNegBig;
+#pragma unroll
+  for (int ch = 0; ch < kColsChunks; ch++) M = fmaxf(M, m[ch]);
+  float L = 0.f, O = 0.f;
+#pragma unroll
+  for (int ch = 0; ch < kColsChunks; ch++) {
+    const float w = exp2f(m[ch] - M);
+    L += l[ch] * w;
+    O += o[ch] * w;
+  }
+  // out = O / L (zero when L = 0, math_util.rs:357, 372), then the gate
+  float r = (L > 0.f) ? O / L : 0.f;
+  const int tok = c >> 3, hq = kvh * 8 + (c & 7);
+  const int64_t oidx = ((int64_t)tok * a.H + hq) * D + d;
+  if (a.gate) r = mi::gate_mul(r, (float)a.gate[oidx]);
+  a.out[oidx] = (_Float16)r;
+}
+
 // Wide verify for more than 4 query tokens (MI_ATTN_VERIFY_WIDE=0, read at
 // each call, turns it off): one split pass that reads every K/V tile once
 // per 16 tokens (attn_prefill64_kernel's MFMA tiles over key chunks), then
@@ -1303,8 +1344,12 @@ mi_status wide_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float1
   c.max_chunks = nchunks;
   c.batch = 1;
   c.nslots = nchunks;
-  MI_HIP(mi::launch("attn_combine", attn_combine_kernel<32>, dim3(n * 8, G * (D / 32), 1),
-                    dim3(256), 0, stream, c));
+  if (nchunks <= kColsChunks)
+    MI_HIP(mi::launch("attn_combine", attn_combine_cols_kernel, dim3(n * 8, G), dim3(D), 0,
+                      stream, c));
+  else
+    MI_HIP(mi::launch("attn_combine", attn_combine_kernel<32>, dim3(n * 8, G * (D / 32), 1),
+                      dim3(256), 0, stream, c));
   return MI_OK;
 }
 

@@ -580,14 +580,19 @@ mi_status launch_verify_wide(const PrefillArgs& a, const VerifyArgs& v, int grid
 }
 
 // Whether mi_attn_prefill takes the split-K form (the wide verify's pass and
-// merge): up to 1024 new tokens after a past of at least 4096 rows and
-// twice the new tokens.  Timed at past 65536: 16 / 128 / 512 new tokens
-// took 1434 / 1446 / 1455 us as the prefill grid.  MI_ATTN_PREFILL_SPLIT=0
-// (read at each call) turns it off.
+// merge): up to 1024 new tokens after a past of at least 2048 rows and
+// twice the new tokens.  Timed, split-K against the prefill grid (µs):
+// past 65536: 16 / 128 / 1024 new tokens 49 / 164 / 1004 against 1434 /
+// 1446 / 1489; past 4096: 64 / 256 / 1024 tokens 36 / 47 / 115 against 105 /
+// 114 / 136; past 2048, 512 tokens 51 against 70.  It loses where the past
+// is short next to n (past 1024, 1024 tokens: 70 against 62; no past, 256
+// tokens: 32 against 20) and beyond 1024 tokens (past 32768, 1536 tokens:
+// 932 against 846).  MI_ATTN_PREFILL_SPLIT=0 (read at each call) turns it
+// off.
 bool prefill_split_k(int64_t past, int32_t n) {
   const char* e = getenv("MI_ATTN_PREFILL_SPLIT");
   if (e && *e && atoi(e) == 0) return false;
-  return n <= 1024 && past >= 4096 && past >= 2 * (int64_t)n;
+  return n <= 1024 && past >= 2048 && past >= 2 * (int64_t)n;
 }
 
 // Queries per wave of the prefill kernel: 64 (attn_prefill64_kernel, the
