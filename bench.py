@@ -373,6 +373,32 @@ def main():
         rec["verify"]["k16_grouped_us_per_layer"] = ms16g * 1000 / nl
         print(f"[bench] verify K=16 {ms16 * 1000 / nl:.2f} us/layer (as 4-token groups "
               f"{ms16g * 1000 / nl:.2f})", file=sys.stderr, flush=True)
+        # Chunked prefill after a long past: 128 new tokens at 65536 rows,
+        # the split-K form (default) against the prefill grid
+        # (MI_ATTN_PREFILL_SPLIT=0).
+        q128 = randn(128, H, D, seed=59)
+        out128 = torch.empty_like(q128)
+
+        def prefill_after_past():
+            for layer in range(nl):
+                cache.set_pos(C5_CTX + 16)
+                mi.attn_prefill(cache, layer, q128, None, None, C5_CTX - 128,
+                                out=out128)
+
+        msp = timed(prefill_after_past, args.steps, args.warmup,
+                    backlog_ms=args.steps * nl * 0.4 + 20)
+        _lib.prof_enable(False)
+        os.environ["MI_ATTN_PREFILL_SPLIT"] = "0"
+        try:
+            mspu = timed(prefill_after_past, max(2, args.steps // 4), 1,
+                         backlog_ms=args.steps * nl * 2.0 + 20)
+        finally:
+            del os.environ["MI_ATTN_PREFILL_SPLIT"]
+        _lib.prof_enable(False)
+        rec["verify"]["prefill128_after_65408_us_per_layer"] = msp * 1000 / nl
+        rec["verify"]["prefill128_after_65408_unsplit_us_per_layer"] = mspu * 1000 / nl
+        print(f"[bench] prefill of 128 tokens after 65408 rows {msp * 1000 / nl:.1f} us/layer "
+              f"(prefill grid {mspu * 1000 / nl:.1f})", file=sys.stderr, flush=True)
         del cache
 
     # ---------------------------------------------------------------- C3 ragged
