@@ -1292,24 +1292,18 @@ bool verify_wide_enabled() {
   return !(e && *e && atoi(e) == 0);
 }
 
-// Chunking of the wide verify: about 256 workgroups of (row block of 16
-// tokens, chunk, KV head); whole 64-key tiles; at most kMaxChunks chunks
-// (the combine's limit).
-struct WidePlan {
+// The wide verify's plan (mi::wide_plan) and the workspace its partials
+// (O, m, l) take.
+struct WideLaunch {
   int64_t chunk;
   int nchunks;
-  size_t ws_bytes;  // partials (O, m, l)
+  size_t ws_bytes;
 };
-WidePlan wide_plan(int G, int64_t past, int32_t n) {
-  const int64_t rows = past + n;
-  const int nrb = (n + 15) / 16;
-  const int64_t target = std::max<int64_t>(1, (256 + (int64_t)G * nrb - 1) / ((int64_t)G * nrb));
-  int64_t chunk = (rows + target - 1) / target;
-  chunk = std::max<int64_t>(chunk, (rows + kMaxChunks - 1) / kMaxChunks);
-  chunk = (chunk + 63) / 64 * 64;
-  WidePlan p;
-  p.chunk = chunk;
-  p.nchunks = (int)((rows + chunk - 1) / chunk);
+WideLaunch wide_launch(int G, int64_t past, int32_t n) {
+  const mi::WidePlan w = mi::wide_plan(G, past, n);
+  WideLaunch p;
+  p.chunk = w.chunk;
+  p.nchunks = w.nchunks;
   p.ws_bytes = (size_t)G * p.nchunks * 8 * n * (D + 2) * sizeof(float) + 256;
   return p;
 }
@@ -1319,7 +1313,7 @@ mi_status wide_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float1
                       const _Float16* k_new, const _Float16* v_new) {
   const int G = kv->G;
   const int64_t rows = past_pos + n;
-  const WidePlan wp = wide_plan(G, past_pos, n);
+  const WideLaunch wp = wide_launch(G, past_pos, n);
   const int64_t chunk = wp.chunk;
   const int nchunks = wp.nchunks;
   const int ncols = 8 * n;
@@ -1437,7 +1431,9 @@ mi_status attend_wide(mi_kv* kv, int32_t layer, const _Float16* q, const _Float1
   return wide_attend(kv, layer, q, gate, out, past, n, stream, nullptr, nullptr);
 }
 
-size_t wide_workspace_bytes(int G, int64_t past, int32_t n) { return wide_plan(G, past, n).ws_bytes; }
+size_t wide_workspace_bytes(int G, int64_t past, int32_t n) {
+  return wide_launch(G, past, n).ws_bytes;
+}
 }  // namespace mi
 
 extern "C" mi_status mi_attn_decode(mi_kv* kv, int32_t layer, const mi_f16* q,

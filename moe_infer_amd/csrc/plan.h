@@ -129,6 +129,29 @@ MI_HD inline WaveTiles split_wave_tiles(int64_t begin, int64_t end, int nwh, int
 // Most chunks (partials) per sequence of one split launch.
 constexpr int kMaxSplitChunks = 1024;
 
+// Chunking of the wide verify / split-K prefill (attn_verify_wide_kernel):
+// about 256 workgroups of (row block of 16 tokens, chunk, KV head) over rows
+// [0, past + n); whole 64-key tiles; at most kMaxSplitChunks chunks (the
+// merge kernels' limit).
+struct WidePlan {
+  int64_t chunk;
+  int nchunks;
+};
+inline WidePlan wide_plan(int G, int64_t past, int n) {
+  const int64_t rows = past + n;
+  const int64_t nrb = (n + 15) / 16;
+  int64_t target = (256 + G * nrb - 1) / (G * nrb);
+  if (target < 1) target = 1;
+  int64_t chunk = (rows + target - 1) / target;
+  const int64_t min_chunk = (rows + kMaxSplitChunks - 1) / kMaxSplitChunks;
+  if (chunk < min_chunk) chunk = min_chunk;
+  chunk = (chunk + kPrefillBK - 1) / kPrefillBK * kPrefillBK;
+  WidePlan p;
+  p.chunk = chunk;
+  p.nchunks = (int)((rows + chunk - 1) / chunk);
+  return p;
+}
+
 struct SplitKnobs {
   int gh;     // KV heads per workgroup (2, or 1 when set to 1)
   int wgs;    // target workgroup count

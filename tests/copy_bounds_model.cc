@@ -62,9 +62,9 @@ static long long prefill_violations(int past, int n, long long cap, bool old_rul
 // The same for attn_prefill64_kernel: every pass (the walk, and after an
 // overflow the max pass and the walk again) copies K(0) first; tile 0's asm
 // block copies K(min(1, nt - 1)) and V(0); at tile t >= 1 an active wave
-// (mi::prefill64_active) copies K(min(t + 1, nt - 1)) and V(t) in its asm
-// block, any other copies K(t + 1) when t + 1 < nt, and V(t) (the max pass:
-// K only).  Both passes are walked.
+// (mi::prefill64_active) copies K(min(t + 1, nt - 1)) in its asm block and
+// V(t) from its PV phase, any other copies K(t + 1) when t + 1 < nt, and
+// V(t) (the max pass: K only).  Both passes are walked.
 static long long prefill64_violations(int past, int n, long long cap) {
   long long bad = 0;
   auto copy = [&](int T) {
@@ -81,11 +81,61 @@ static long long prefill64_violations(int past, int n, long long cap) {
           const int tk = t + 1 < nt ? t + 1 : t;
           if (t == 0 || mi::prefill64_active(p, t)) {
             copy(tk);
-            copy(t);  // V(t), also in the max pass's asm block
+            if (pass == 0) copy(t);  // V(t)
           } else {
             if (t + 1 < nt) copy(t + 1);
             if (pass == 0) copy(t);
           }
+        }
+      }
+    }
+  return bad;
+}
+
+// The wide verify / split-K prefill (attn_verify_wide_kernel): plan
+// mi::wide_plan (two KV heads); workgroup (row block rb of 16 tokens, chunk
+// c): keys from kbeg = c * chunk, wave (qb, kp) walking mi::verify_wave64's
+// tiles with the 64-query kernel's copies (K(0) first; then K(min(t + 1,
+// nt - 1)) and V(t) at tile 0 and on active tiles, else K(t + 1) when
+// t + 1 < nt and V(t); the max pass copies K only), tile T being rows
+// [kbeg + 64 T, + 64).  Every copy must lie inside `cap` rows, the chunks
+// must be whole tiles, at most kMaxSplitChunks, and cover [0, past + n),
+// and each token's visible keys within a chunk must lie inside the tiles
+// its workgroup walks.
+static long long wide_violations(long long past, int n, long long cap) {
+  const mi::WidePlan wp = mi::wide_plan(2, past, n);
+  long long bad = 0;
+  if (wp.chunk % mi::kPrefillBK || wp.nchunks > mi::kMaxSplitChunks ||
+      (long long)wp.nchunks * wp.chunk < past + n)
+    bad++;
+  const int nrb = (n + 15) / 16;
+  for (int rb = 0; rb < nrb; rb++)
+    for (int c = 0; c < wp.nchunks; c++) {
+      const long long kbeg = (long long)c * wp.chunk;
+      auto copy = [&](int T) {
+        if (kbeg + (long long)T * mi::kPrefillBK + mi::kPrefillBK > cap) bad++;
+      };
+      for (int w = 0; w < 4; w++) {
+        const mi::PrefillWave64 p = mi::verify_wave64(past, n, kbeg, wp.chunk, 16 * rb, w & 1, w >> 1);
+        const int nt = p.nt;
+        for (int pass = 0; pass < 2; pass++) {
+          copy(0);
+          for (int t = 0; t < nt; t++) {
+            const int tk = t + 1 < nt ? t + 1 : t;
+            if (t == 0 || mi::prefill64_active(p, t)) {
+              copy(tk);
+              if (pass == 0) copy(t);
+            } else {
+              if (t + 1 < nt) copy(t + 1);
+              if (pass == 0) copy(t);
+            }
+          }
+        }
+        // tokens of this wave's rows: tok0 + 8 qb .. + 7
+        for (int i = 16 * rb + 8 * (w & 1); i < 16 * rb + 8 * (w & 1) + 8 && i < n; i++) {
+          long long vis_end = past + i + 1;  // keys [0, past + i]
+          if (vis_end > kbeg + wp.chunk) vis_end = kbeg + wp.chunk;
+          if (vis_end > kbeg && vis_end > kbeg + p.kv_len) bad++;
         }
       }
     }
@@ -154,5 +204,14 @@ int main() {
       }
     }
   std::printf("split %lld %lld\n", cs, bs);
+
+  long long cw = 0, bw = 0;
+  for (long long past : {0LL, 1LL, 63LL, 64LL, 65LL, 700LL, 2048LL, 4096LL, 20000LL, 65536LL,
+                         131071LL})
+    for (int n = 1; n <= 1100; n += (n < 40 ? 1 : 37)) {
+      bw += wide_violations(past, n, round_cap(past + n));
+      cw++;
+    }
+  std::printf("wide %lld %lld\n", cw, bw);
   return 0;
 }

@@ -3,8 +3,10 @@ by a model of their tile walks compiled against the launch-plan header the
 kernels themselves use (moe_infer_amd/csrc/plan.h): the causal prefill's
 global -> LDS tile copies (both kernel forms, the 64-query one over both of
 its passes) over (past, n) in [0, 700)^2 and at long pasts,
-and the split-K decode / verify tile loads over lengths 1..5000 and long
-contexts under several planning knobs.  The prefill walk without the
+the split-K decode / verify tile loads over lengths 1..5000 and long
+contexts under several planning knobs, and the wide verify / split-K
+prefill's tile copies (mi::wide_plan, mi::verify_wave64) over pasts up to
+131071 and 1..1100 tokens.  The prefill walk without the
 steady schedule's last-tile rule must find out-of-allocation copies (the
 fault that rule fixed), so the model is shown to catch it."""
 import shutil
@@ -56,3 +58,10 @@ def test_prefill_long_past_and_c4_sizes(model_output):
 def test_split_tiles_are_whole_and_inside_the_allocation(model_output):
     cases, bad = model_output["split"]
     assert cases > 0 and bad == 0
+
+
+def test_wide_verify_tiles_stay_inside_the_allocation(model_output):
+    """The wide verify / split-K prefill: every tile copy inside the cache,
+    chunks whole tiles covering every row, each token's visible keys walked."""
+    cases, bad = model_output["wide"]
+    assert cases > 500 and bad == 0
