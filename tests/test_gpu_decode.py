@@ -110,7 +110,8 @@ def test_engine_step_sequence():
 
 @pytest.mark.parametrize("n,past", [(1, 0), (2, 5), (3, 31), (4, 61), (4, 255), (7, 100),
                                     (9, 1000), (6, 20000), (16, 0), (5, 59), (16, 61),
-                                    (13, 4093), (12, 4096), (16, 20000)])
+                                    (13, 4093), (12, 4096), (16, 20000), (17, 0), (33, 100),
+                                    (40, 5000)])
 def test_verify_matches_causal_oracle(n, past):
     announce(f"verify n={n} past={past}")
     rng = np.random.default_rng(1000 * n + past)
@@ -264,6 +265,49 @@ def test_graph_replay_of_steps_matches_eager():
             assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"replay {r}"
     assert_close(out1, O.decode(host(q), k[:L + 1], v[:L + 1], L + 1, gate=host(g)),
                  "graph step vs oracle")
+
+
+def test_graph_replay_of_wide_verify_and_split_prefill():
+    """The wide verify (8 tokens) and the split-K prefill (40 tokens after a
+    past of 6008 rows), each an append, a split pass and a merge, captured in
+    one HIP graph after an eager call sized the workspace: every replay, with
+    eager work between, equals the eager outputs bit for bit, and those match
+    the oracle."""
+    from moe_infer_amd import attn_prefill
+    announce("graph replay of wide verify / split-K prefill")
+    rng = np.random.default_rng(33)
+    L, n8, n40 = 6000, 8, 40
+    k, v = f16(rng, L + n8 + n40, G * D), f16(rng, L + n8 + n40, G * D)
+    c = filled_cache(k[:L], v[:L], capacity=L + n8 + n40)
+    q8, g8 = dev(f16(rng, n8, H, D)), dev(f16(rng, n8, H, D))
+    q40 = dev(f16(rng, n40, H, D))
+    k8, v8 = dev(k[L:L + n8]), dev(v[L:L + n8])
+    k40, v40 = dev(k[L + n8:]), dev(v[L + n8:])
+    o8 = torch.empty(n8, H, D, dtype=torch.float16, device="cuda")
+    o40 = torch.empty(n40, H, D, dtype=torch.float16, device="cuda")
+
+    def step():
+        attn_verify(c, 0, q8, k8, v8, L, gate=g8, out=o8)
+        attn_prefill(c, 0, q40, k40, v40, L + n8, out=o40)
+
+    step()  # eager: sizes the workspace, sets the kernels' LDS limits
+    torch.cuda.synchronize()
+    ref = [o8.clone(), o40.clone()]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    other = filled_cache(k[:300], v[:300])
+    for r in range(4):
+        for o in (o8, o40):
+            o.fill_(7.0)
+        graph.replay()
+        attn_decode(other, 0, q8[0], 300)  # eager work between the replays
+        torch.cuda.synchronize()
+        for a, b in zip(ref, (o8, o40)):
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"replay {r}"
+    assert_close(o8, O.causal(host(q8), k[:L + n8], v[:L + n8], L, gate=host(g8)),
+                 "graph wide verify vs oracle")
+    assert_close(o40, O.causal(host(q40), k, v, L + n8), "graph split-K prefill vs oracle")
 
 
 def test_graph_survives_workspace_growth_on_the_same_handle():
