@@ -89,10 +89,11 @@ class EngineSnapshot:
     mtp_pos: int
 
 
-# Largest token count forward_batched sends to the split-K verify kernel: it
-# reads the cache once per 4 tokens, which beats the prefill kernel (one
-# workgroup per (query tile, head)) when the new tokens are few and the cache
-# is long, the speculative-verify case.
+# Largest token count forward_batched sends to mi_attn_verify (split-K over
+# the cache: the decode kernel's form up to 4 tokens, the prefill tiles'
+# split-K form above), the speculative-verify case; more tokens go to
+# mi_attn_prefill, which itself splits over the past when the past is long
+# next to them.
 VERIFY_MAX_TOKENS = 16
 
 
