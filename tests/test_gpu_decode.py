@@ -377,3 +377,34 @@ def test_gate_extremes_decode_and_prefill():
     c2 = Cache(num_layers=1, capacity=n)
     outp = attn_prefill(c2, 0, dev(qn), dev(kn), dev(vn), 0, gate=dev(gn))
     assert_close(outp, O.causal(qn, kn, vn, 0, gate=gn), "prefill gate extremes")
+
+
+@pytest.mark.parametrize("Hq,Gk", [(32, 4), (8, 1)])
+def test_other_head_counts(Hq, Gk):
+    """Head counts other than 16 / 2 (eight query heads per KV head, the
+    kernels' group size): decode, verify of 4 and 12 tokens (the grouped and
+    wide forms) and prefill (its grid, and its split-K form after a long
+    past) against the oracle."""
+    from moe_infer_amd import attn_prefill
+    announce(f"head counts H={Hq} G={Gk}")
+    rng = np.random.default_rng(Hq + Gk)
+    L = 3000
+    k, v = f16(rng, L + 64, Gk * D), f16(rng, L + 64, Gk * D)
+    c = Cache(num_layers=1, num_q_heads=Hq, num_kv_heads=Gk, capacity=L + 64)
+    c.upload(0, k[:L], v[:L])
+    c.set_pos(L)
+    q1, g1 = f16(rng, Hq * D), f16(rng, Hq * D)
+    out = attn_decode(c, 0, dev(q1), L, gate=dev(g1))
+    assert_close(out, O.decode(q1, k, v, L, gate=g1, H=Hq, G=Gk), f"decode H={Hq}")
+    for n in (4, 12):
+        q, g = f16(rng, n, Hq, D), f16(rng, n, Hq, D)
+        c.set_pos(L)
+        out = attn_verify(c, 0, dev(q), dev(k[L:L + n]), dev(v[L:L + n]), L, gate=dev(g))
+        ref = O.causal(q, k[:L + n], v[:L + n], L, gate=g, H=Hq, G=Gk)
+        assert_close(out, ref, f"verify n={n} H={Hq}")
+    for past, n in ((0, 300), (2500, 40)):  # the grid; the split-K form
+        q = f16(rng, n, Hq, D)
+        c.set_pos(past)
+        out = attn_prefill(c, 0, dev(q), dev(k[past:past + n]), dev(v[past:past + n]), past)
+        ref = O.causal(q, k[:past + n], v[:past + n], past, H=Hq, G=Gk)
+        assert_close(out, ref, f"prefill past={past} n={n} H={Hq}")
