@@ -1237,11 +1237,6 @@ mi_status run_split(const _Float16* k, const _Float16* v, const int32_t* offsets
   return MI_OK;
 }
 
-// Verify / decode over the cache: n query tokens at positions past_pos ..
-// past_pos+n-1, rows [0, past_pos+n) already in the cache.
-// With k_new / v_new, the n new rows [past_pos, past_pos + n) are appended
-// by the split kernels themselves (each token group appends its own rows,
-// which precede every read of them); the caller has grown the cache.
 // Merge of a few chunks (at most kColsChunks) for many columns: one thread
 // per output value, one workgroup of D threads per (column, KV head).  The
 // wide verify's partials for many tokens come in few chunks, where
@@ -1347,6 +1342,12 @@ mi_status wide_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float1
   return MI_OK;
 }
 
+// Verify / decode over the cache: n query tokens at positions past_pos ..
+// past_pos+n-1, rows [0, past_pos+n) already in the cache.
+// With k_new / v_new, the n new rows [past_pos, past_pos + n) are appended
+// by the split kernels themselves (each token group appends its own rows,
+// which precede every read of them; the wide form appends them all in a
+// launch of their own first); the caller has grown the cache.
 mi_status cache_attend(mi_kv* kv, int32_t layer, const _Float16* q, const _Float16* gate,
                        _Float16* out, int64_t past_pos, int32_t n, hipStream_t stream,
                        const _Float16* k_new = nullptr, const _Float16* v_new = nullptr) {
