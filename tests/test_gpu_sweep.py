@@ -55,6 +55,27 @@ def test_verify_random_shapes(seed):
     assert_close(out, ref, f"sweep verify seed={seed}")
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_split_prefill_and_wide_verify_random_shapes(seed):
+    """Prefill after a past of 2048 rows or more (at most half of it new)
+    takes the split-K form, and verify of more than 4 tokens the wide form:
+    both run the prefill tiles over key chunks and merge the partials.
+    Random (past, n) with unaligned chunk ends, against the oracle."""
+    rng = np.random.default_rng(3000 + seed)
+    past = int(rng.integers(2048, 6000))
+    n = int(rng.integers(5, 100))
+    gated = bool(seed % 2)
+    use_verify = seed % 4 >= 2
+    announce(f"sweep split-K seed={seed} past={past} n={n} gated={gated} verify={use_verify}")
+    c, kp, vp = _filled(rng, past, past + n)
+    q, k, v, g = f16(rng, n, H, D), f16(rng, n, G * D), f16(rng, n, G * D), f16(rng, n, H, D)
+    call = attn_verify if use_verify else attn_prefill
+    out = call(c, 0, dev(q), dev(k), dev(v), past, gate=dev(g) if gated else None)
+    ref = O.causal(q, np.concatenate([kp, k]), np.concatenate([vp, v]), past,
+                   gate=g if gated else None)
+    assert_close(out, ref, f"sweep split-K seed={seed}")
+
+
 @pytest.mark.parametrize("seed", range(6))
 def test_decode_random_lengths_after_appends(seed):
     """The cache is filled by several appends of random sizes (growth on the
